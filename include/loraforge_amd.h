@@ -1,0 +1,144 @@
+/*
+ * loraforge_amd -- C ABI of the MI355X (gfx950) NF4 + multi-LoRA serving path.
+ *
+ * Every entry point takes raw device pointers, element counts/strides and a
+ * HIP stream (passed as void*, NULL = the null stream), launches
+ * asynchronously on that stream, allocates nothing and returns an int status:
+ *   LF_OK (0), LF_EINVAL (1, argument/layout contract -> ValueError),
+ *   LF_EHIP (2, HIP runtime error -> RuntimeError).
+ * lf_last_error() returns the calling thread's message for the last failure.
+ * bf16 tensors are passed as uint16_t bit patterns. Device metadata values are
+ * trusted (never read back to the host), so calls are graph-capturable.
+ *
+ * Reference citations are relative to the reference tree
+ * (lishenghui/loraforge, src/loraforge/...).
+ */
+#ifndef LORAFORGE_AMD_H
+#define LORAFORGE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LF_ABI_VERSION 1
+#define LF_OK 0
+#define LF_EINVAL 1
+#define LF_EHIP 2
+
+const char* lf_last_error(void);
+int lf_abi_version(void);
+/* gcnArchName of a device (e.g. "gfx950:sramecc+:xnack-"). */
+int lf_device_arch(int device, char* name, int capacity);
+
+/* --------------------------------------------------------------------------
+ * NF4 dequantisation.
+ * Replaces the Triton launch of ops/nf4.py:7-38 (_dequantize, byte-pair
+ * kernel ops/_nf4_kernels.py:44-61) behind dequantize_nf4 (ops/nf4.py:44).
+ * out[e] = bf16_rne(code[nibble(e)] * scales[e / 64]); nibble(e) is the high
+ * nibble of byte e/2 for even e, the low nibble for odd e.
+ * numel = N*K, a positive multiple of 4096. qweight 4-byte aligned, out
+ * 16-byte aligned.
+ * ------------------------------------------------------------------------ */
+int lf_nf4_dequant(const uint8_t* qweight, const float* scales, const float* code, uint16_t* out,
+                   int64_t numel, void* stream);
+
+/* Same, with double-quantised block scales reconstructed in-kernel as
+ * fl32(fl32(code2[absmax_q[j]] * absmax2[j / dq_block]) + *offset)
+ * (ops/nf4.py:144-147, prepare_scales nested branch). offset is a device
+ * pointer to one fp32; code2 holds 256 fp32. */
+int lf_nf4_dequant_dq(const uint8_t* qweight, const uint8_t* absmax_q, const float* absmax2,
+                      const float* code2, const float* offset, int64_t dq_block, const float* code,
+                      uint16_t* out, int64_t numel, void* stream);
+
+/* prepare_scales (ops/nf4.py:109-148) nested branch: writes the nblocks fp32
+ * scales that bitsandbytes dequantize_blockwise(absmax, state2) + offset
+ * produces, without bitsandbytes. */
+int lf_nf4_prepare_scales_dq(const uint8_t* absmax_q, const float* absmax2, const float* code2,
+                             const float* offset, int64_t dq_block, float* scales, int64_t nblocks,
+                             void* stream);
+
+/* --------------------------------------------------------------------------
+ * Retained-rank row operators.
+ * lf_row_shrink replaces the pybind `shrink` of ops/csrc/lora_rows.cu:172-186
+ * (row_shrink, ops/lora_rows.py:54-109): x [tokens, width] with row stride
+ * x_stride; a [G, num_slices*capacity, width] contiguous; z [tokens,
+ * num_slices*capacity] contiguous; slots int32 [tokens]; ranks int32 [G].
+ * ------------------------------------------------------------------------ */
+int lf_row_shrink(const uint16_t* x, const uint16_t* a, uint16_t* z, const int32_t* slots,
+                  const int32_t* ranks, int64_t tokens, int64_t width, int64_t x_stride,
+                  int32_t num_slices, int64_t capacity, int32_t max_rank, void* stream);
+
+/* lf_row_expand replaces the pybind `expand` of ops/csrc/lora_rows.cu:188-209
+ * (row_expand, ops/lora_rows.py:115-239); arguments keep that binding's
+ * order and meaning. b_strides is the reference's "buckets". */
+int lf_row_expand(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets,
+                  const int32_t* b_strides, uint16_t* y, const int32_t* segment_indptr,
+                  const int32_t* segment_slots, const int32_t* token_indices, const int32_t* ranks,
+                  const float* scales, const int32_t* slice_offsets, const int32_t* segment_count,
+                  int64_t tokens, int64_t out_width, int64_t y_stride, int32_t num_slices,
+                  int64_t capacity, int32_t blocks, int32_t threads, void* stream);
+
+/* --------------------------------------------------------------------------
+ * Fused NF4 base linear + per-token multi-LoRA (one launch for decode).
+ * Replaces the three-call sequence of the reference serving path:
+ *   integrations/_sglang_nf4_linear.py:116-129 (dequant -> F.linear -> +bias),
+ *   ops/rowexpand.py:34-39 / ops/lora_rows.py:54 (shrink),
+ *   ops/rowexpand.py:42-92 / ops/lora_rows.py:115 (expand).
+ * y[m, n] = bf16(x[m] . W[n]) (+bias, bf16) then, for token m with slot
+ * g = token_slots[m] >= 0 and r = ranks[g] > 0, column n in slice s:
+ *   z = bf16(A_g[s*r + j] . x[m]),
+ *   y[m, n] = bf16(y[m, n] + bf16(scales[g] * sum_j z[s*r + j] * B_g[n, j])).
+ * A_g: num_slices*r rows of width K at element a_offsets[g] of a_store.
+ * B_g: [N, b_strides[g]] at element b_offsets[g] of b_store (zero padded).
+ * ------------------------------------------------------------------------ */
+typedef struct lf_nf4_weight {
+  const uint8_t* qweight; /* [N*K/2] */
+  const float* scales;    /* fp32 [N*K/64], or NULL when double-quantised */
+  const uint8_t* absmax_q;/* uint8 [N*K/64] (double quant) */
+  const float* absmax2;   /* fp32 [ceil(N*K/64/dq_block)] */
+  const float* code2;     /* fp32 [256] */
+  const float* offset;    /* fp32 [1] */
+  int64_t dq_block;
+  const float* code;      /* fp32 [16] */
+  int64_t n;              /* output features, multiple of 64 */
+  int64_t k;              /* input features, multiple of 64 */
+} lf_nf4_weight;
+
+typedef struct lf_lora {
+  const uint16_t* a_store;
+  const int64_t* a_offsets;   /* [G] element offsets, multiples of 8 */
+  const uint16_t* b_store;
+  const int64_t* b_offsets;   /* [G] element offsets, multiples of 8 */
+  const int32_t* b_strides;   /* [G] power of two in 1..64, >= rank */
+  const int32_t* ranks;       /* [G] 0..max_rank */
+  const float* scales;        /* [G] */
+  const int32_t* token_slots; /* [M] slot or -1 */
+  const int32_t* slice_offsets; /* [num_slices+1] */
+  int32_t num_slices;         /* 1..3 */
+  int32_t max_rank;           /* 1..64 */
+} lf_lora;
+
+/* Bytes of device workspace lf_nf4_lora_linear needs for this problem. The
+ * first 256 bytes hold counters that must be zero before the first call;
+ * every completed call leaves them zero again. Calls that share one
+ * workspace must not overlap in time. */
+int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices, int32_t max_rank);
+
+/* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);
+ * y [m, N] bf16 with row stride y_stride; bias bf16 [N] or NULL;
+ * lora NULL for the base linear alone. */
+int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* weight,
+                       const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Reads the workspace status word written by the last call (0 = ok); for
+ * tests and diagnostics only (synchronises the stream). */
+int lf_nf4_lora_status(const void* workspace, void* stream, int32_t* status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LORAFORGE_AMD_H */

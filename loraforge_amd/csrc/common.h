@@ -1,0 +1,84 @@
+// Shared device helpers and host error plumbing for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+namespace lf {
+
+// ---------------------------------------------------------------------------
+// Status codes returned by every extern "C" entry point.
+// ---------------------------------------------------------------------------
+enum Status : int {
+  kOk = 0,
+  kInvalid = 1,  // argument / layout contract violated (maps to ValueError)
+  kHip = 2,      // HIP runtime error (maps to RuntimeError)
+};
+
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+int hip_status(hipError_t err, const char* what);
+
+#define LF_REQUIRE(cond, ...)                  \
+  do {                                         \
+    if (!(cond)) return ::lf::fail(::lf::kInvalid, __VA_ARGS__); \
+  } while (0)
+
+#define LF_HIP(call)                                     \
+  do {                                                   \
+    hipError_t lf_err_ = (call);                         \
+    if (lf_err_ != hipSuccess) return ::lf::hip_status(lf_err_, #call); \
+  } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// Vector types used for MFMA operands and 128-bit memory traffic.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 bits -> fp32 (exact).
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+// Two fp32 -> packed bf16 pair (low half = a), round-to-nearest-even.
+// gfx950 lowers this to one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 v = __builtin_convertvector((f32x2){a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// fp32 -> bf16 bits, round-to-nearest-even.
+__device__ __forceinline__ uint32_t f32_to_bf16(float a) { return pack_bf16x2(a, 0.0f) & 0xffffu; }
+
+// fp32 -> nearest bf16 value, returned as fp32.
+__device__ __forceinline__ float round_bf16(float a) { return bf16_to_f32(f32_to_bf16(a)); }
+
+// One 16x16x32 bf16 MFMA step: acc[i = 4*(lane/16) + r][j = lane%16] +=
+// sum_k a[i][k] * b[k][j], where lane l supplies a[l%16][8*(l/16) .. +8)
+// and b[8*(l/16) .. +8)[l%16].
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Wave-wide fp32 sum (wave64) through cross-lane shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+}  // namespace lf

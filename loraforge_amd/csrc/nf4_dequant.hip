@@ -1,0 +1,113 @@
+// Standalone NF4 -> bf16 dequantisation (reference: ops/nf4.py:7-38 and
+// ops/_nf4_kernels.py:44-61, the byte-pair kernel) and the double-quant scale
+// reconstruction of prepare_scales (ops/nf4.py:144-147).
+//
+// HBM-bound: per 64-element block it reads 32 packed bytes + 4 scale bytes
+// and writes 128 bytes. Each lane decodes one packed dword (8 elements) per
+// step and stores 16 bytes, so every load (256 B/wave) and store (1 KiB/wave)
+// instruction is fully coalesced. Four independent steps per lane keep
+// enough bytes in flight.
+#include "nf4_common.h"
+#include "../../include/loraforge_amd.h"
+
+namespace lf {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kSteps = 4;
+
+template <bool kDouble>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(const uint32_t* __restrict__ packed,
+                                                               ScaleSource src, const float* __restrict__ code,
+                                                               uint4* __restrict__ out, int64_t ndwords) {
+  __shared__ float table[16];
+  __shared__ float code2[kDouble ? 256 : 1];
+  if (threadIdx.x < 16) table[threadIdx.x] = code[threadIdx.x];
+  if constexpr (kDouble) code2[threadIdx.x] = src.code2[threadIdx.x];
+  __syncthreads();
+  const float offset = kDouble ? *src.offset : 0.0f;
+  const int64_t base = int64_t(blockIdx.x) * (kThreads * kSteps) + threadIdx.x;
+  uint32_t words[kSteps];
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int64_t w = base + s * kThreads;
+    words[s] = w < ndwords ? packed[w] : 0u;
+  }
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int64_t w = base + s * kThreads;
+    if (w < ndwords) {
+      // 8 elements per dword, 64 per block: block = w / 8.
+      const float scale = block_scale(src, w >> 3, code2, offset);
+      out[w] = decode_dword(words[s], scale, table);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void dq_scales_kernel(ScaleSource src, float* __restrict__ scales,
+                                                             int64_t nblocks) {
+  __shared__ float code2[256];
+  code2[threadIdx.x] = src.code2[threadIdx.x];
+  __syncthreads();
+  const float offset = *src.offset;
+  for (int64_t j = int64_t(blockIdx.x) * kThreads + threadIdx.x; j < nblocks;
+       j += int64_t(gridDim.x) * kThreads) {
+    scales[j] = block_scale(src, j, code2, offset);
+  }
+}
+
+int launch_dequant(const uint8_t* qweight, const ScaleSource& src, const float* code, uint16_t* out,
+                   int64_t numel, void* stream) {
+  LF_REQUIRE(numel > 0 && numel % (kNf4Block * kNf4Block) == 0,
+             "element count must be a positive multiple of 4096");
+  LF_REQUIRE(qweight && code && out, "null pointer argument");
+  LF_REQUIRE(aligned16(out) && (reinterpret_cast<uintptr_t>(qweight) & 3u) == 0,
+             "packed bytes must be 4-byte aligned and out 16-byte aligned");
+  const int64_t ndwords = numel / 8;
+  const int64_t grid = (ndwords + kThreads * kSteps - 1) / (kThreads * kSteps);
+  LF_REQUIRE(grid < (int64_t(1) << 31), "tensor too large");
+  auto s = static_cast<hipStream_t>(stream);
+  const auto* packed = reinterpret_cast<const uint32_t*>(qweight);
+  auto* o = reinterpret_cast<uint4*>(out);
+  if (src.scales) {
+    hipLaunchKernelGGL(nf4_dequant_kernel<false>, dim3(grid), dim3(kThreads), 0, s, packed, src, code, o, ndwords);
+  } else {
+    hipLaunchKernelGGL(nf4_dequant_kernel<true>, dim3(grid), dim3(kThreads), 0, s, packed, src, code, o, ndwords);
+  }
+  LF_HIP(hipGetLastError());
+  return kOk;
+}
+
+}  // namespace
+}  // namespace lf
+
+extern "C" int lf_nf4_dequant(const uint8_t* qweight, const float* scales, const float* code, uint16_t* out,
+                              int64_t numel, void* stream) {
+  LF_REQUIRE(scales != nullptr, "scales required");
+  lf::ScaleSource src{scales, nullptr, nullptr, nullptr, nullptr, 1};
+  return lf::launch_dequant(qweight, src, code, out, numel, stream);
+}
+
+extern "C" int lf_nf4_dequant_dq(const uint8_t* qweight, const uint8_t* absmax_q, const float* absmax2,
+                                 const float* code2, const float* offset, int64_t dq_block, const float* code,
+                                 uint16_t* out, int64_t numel, void* stream) {
+  LF_REQUIRE(absmax_q && absmax2 && code2 && offset, "double-quant state pointers required");
+  LF_REQUIRE(dq_block > 0 && dq_block <= (int64_t(1) << 30), "dq_block must be positive");
+  lf::ScaleSource src{nullptr, absmax_q, absmax2, code2, offset, int(dq_block)};
+  return lf::launch_dequant(qweight, src, code, out, numel, stream);
+}
+
+extern "C" int lf_nf4_prepare_scales_dq(const uint8_t* absmax_q, const float* absmax2, const float* code2,
+                                        const float* offset, int64_t dq_block, float* scales, int64_t nblocks,
+                                        void* stream) {
+  LF_REQUIRE(absmax_q && absmax2 && code2 && offset && scales, "null pointer argument");
+  LF_REQUIRE(dq_block > 0 && dq_block <= (int64_t(1) << 30), "dq_block must be positive");
+  LF_REQUIRE(nblocks > 0, "nblocks must be positive");
+  lf::ScaleSource src{nullptr, absmax_q, absmax2, code2, offset, int(dq_block)};
+  const int64_t want = (nblocks + lf::kThreads - 1) / lf::kThreads;
+  const int grid = int(want < 4096 ? want : 4096);
+  hipLaunchKernelGGL(lf::dq_scales_kernel, dim3(grid), dim3(lf::kThreads), 0, static_cast<hipStream_t>(stream),
+                     src, scales, nblocks);
+  LF_HIP(hipGetLastError());
+  return lf::kOk;
+}

@@ -1,0 +1,59 @@
+// C-ABI entry of the fused NF4 + multi-LoRA linear: argument validation and
+// dispatch between the decode kernel (M <= 64 tokens) and the prefill GEMM.
+#include "nf4_common.h"
+#include "../../include/loraforge_amd.h"
+
+namespace lf {
+int decode_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
+int launch_nf4_lora_decode(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
+                           const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
+int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
+                            const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+constexpr int64_t kDecodeMaxTokens = 64;
+}  // namespace lf
+
+extern "C" int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices,
+                                              int32_t max_rank) {
+  if (m < 0 || n <= 0 || k <= 0 || num_slices < 1 || max_rank < 1) return -1;
+  if (m <= lf::kDecodeMaxTokens) return lf::decode_workspace_bytes(m, n, k, num_slices, max_rank);
+  return lf::prefill_workspace_bytes(m, n, k, num_slices, max_rank);
+}
+
+extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
+                                  const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  LF_REQUIRE(w != nullptr, "weight descriptor required");
+  LF_REQUIRE(m >= 0 && m < (int64_t(1) << 31), "token count out of range");
+  const int64_t n = w->n, k = w->k;
+  LF_REQUIRE(n > 0 && k > 0 && n % 64 == 0 && k % 64 == 0, "weight shape must contain two positive multiples of 64");
+  LF_REQUIRE(n < (int64_t(1) << 28) && k < (int64_t(1) << 28), "weight shape too large");
+  if (m == 0) return lf::kOk;
+  LF_REQUIRE(x && y && w->qweight && w->code, "null pointer argument");
+  LF_REQUIRE(w->scales || (w->absmax_q && w->absmax2 && w->code2 && w->offset && w->dq_block > 0),
+             "scales or a complete double-quant state required");
+  LF_REQUIRE(lf::aligned16(x) && x_stride >= k && x_stride % 8 == 0, "x must be 16-byte aligned with row stride %% 8 == 0");
+  LF_REQUIRE(lf::aligned16(w->qweight), "packed weight must be 16-byte aligned");
+  LF_REQUIRE(y_stride >= n, "output row stride must cover the output width");
+  if (lora) {
+    LF_REQUIRE(lora->num_slices >= 1 && lora->num_slices <= 3, "num_slices must be in 1..3");
+    LF_REQUIRE(lora->max_rank >= 1 && lora->max_rank <= 64, "max_rank must be in 1..64");
+    LF_REQUIRE(lora->a_store && lora->a_offsets && lora->b_store && lora->b_offsets && lora->b_strides &&
+                   lora->ranks && lora->scales && lora->token_slots && lora->slice_offsets,
+               "incomplete LoRA descriptor");
+    LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
+  }
+  if (m <= lf::kDecodeMaxTokens)
+    return lf::launch_nf4_lora_decode(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, stream);
+  return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int lf_nf4_lora_status(const void* workspace, void* stream, int32_t* status) {
+  LF_REQUIRE(workspace && status, "null pointer argument");
+  auto s = static_cast<hipStream_t>(stream);
+  LF_HIP(hipMemcpyAsync(status, static_cast<const char*>(workspace) + 8, 4, hipMemcpyDeviceToHost, s));
+  LF_HIP(hipStreamSynchronize(s));
+  return lf::kOk;
+}

@@ -1,0 +1,20 @@
+"""gfx950 operators of the NF4 + multi-LoRA serving path (mirror of ``loraforge.ops``)."""
+
+from .fused import LoraBatch, nf4_lora_linear, segments_to_slots, workspace_bytes
+from .lora_rows import row_expand, row_shrink
+from .nf4 import NF4State, NestedState, dequantize_nf4, dequantize_nf4_nested, prepare_scales, quantize_nf4
+
+__all__ = [
+    "LoraBatch",
+    "NF4State",
+    "NestedState",
+    "dequantize_nf4",
+    "dequantize_nf4_nested",
+    "nf4_lora_linear",
+    "prepare_scales",
+    "quantize_nf4",
+    "row_expand",
+    "row_shrink",
+    "segments_to_slots",
+    "workspace_bytes",
+]

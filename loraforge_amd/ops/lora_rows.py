@@ -1,0 +1,204 @@
+"""BF16 retained-rank shrink and compact-B RowExpand on gfx950.
+
+Mirror of ``loraforge.ops.row_shrink`` / ``row_expand``
+(``src/loraforge/ops/lora_rows.py:51-239``): same signatures, layouts,
+metadata contract and exception messages; the kernels are the HIP ones in
+``csrc/row_ops.hip`` reached through the C ABI. Device metadata values are
+trusted inputs; structural validation never copies metadata to the CPU or
+synchronises the stream.
+"""
+
+from __future__ import annotations
+
+from typing import TYPE_CHECKING
+
+from .. import _lib
+from ..annotations import ExperimentalAPI
+from ._checks import distinct_output, require_arch, tensor, vector
+
+if TYPE_CHECKING:
+    from torch import Tensor
+
+
+@ExperimentalAPI(reason="BF16 retained-rank inference operator; gfx950 HIP kernel, caller-owned device metadata.")
+def row_shrink(
+    x: Tensor,
+    a: Tensor,
+    output: Tensor,
+    slots: Tensor,
+    ranks: Tensor,
+    *,
+    num_slices: int = 1,
+    max_rank: int = 64,
+) -> None:
+    """Write live packed A @ x prefixes in place, rounding FP32 sums to BF16.
+
+    x is [tokens, width], A [slots, slices * capacity, width], output
+    [tokens, slices * capacity]. For slot rank r, slice s starts at s*r in
+    both A and output. Slots -1 and rank-zero rows are left unchanged; unused
+    output columns are also unchanged. All live ranks must be <= max_rank.
+    Input width and row stride must be multiples of eight BF16 elements.
+    """
+    import torch
+
+    tensor(x, "x", 2, torch.bfloat16)
+    tensor(a, "a", 3, torch.bfloat16, x.device)
+    tensor(output, "output", 2, torch.bfloat16, x.device)
+    if type(num_slices) is not int or not 1 <= num_slices <= 3:
+        raise ValueError("num_slices must be in 1..3")
+    if type(max_rank) is not int or not 1 <= max_rank <= 64:
+        raise ValueError("max_rank must be in 1..64")
+    if (
+        a.shape[0] < 1
+        or a.shape[1] % num_slices
+        or a.shape[1] // num_slices < max_rank
+        or a.shape[2] != x.shape[1]
+        or output.shape != (x.shape[0], a.shape[1])
+    ):
+        raise ValueError("A/output shapes must agree with slices and rank capacity")
+    if (
+        x.shape[1] < 1
+        or x.shape[1] % 8
+        or x.stride(1) != 1
+        or x.stride(0) < x.shape[1]
+        or x.stride(0) % 8
+        or x.data_ptr() % 16
+        or a.data_ptr() % 16
+        or not a.is_contiguous()
+        or not output.is_contiguous()
+    ):
+        raise ValueError("expected aligned A/x and contiguous A/output")
+    vector(slots, "slots", torch.int32, x.device, x.shape[0])
+    vector(ranks, "ranks", torch.int32, x.device, a.shape[0])
+    distinct_output(output, (x, a, slots, ranks))
+    if x.shape[0] == 0:
+        return
+    require_arch(x.device)
+    lib = _lib.library()
+    with torch.cuda.device(x.device):
+        _lib.check(
+            lib.lf_row_shrink(
+                x.data_ptr(),
+                a.data_ptr(),
+                output.data_ptr(),
+                slots.data_ptr(),
+                ranks.data_ptr(),
+                x.shape[0],
+                x.shape[1],
+                x.stride(0),
+                num_slices,
+                a.shape[1] // num_slices,
+                max_rank,
+                _lib.stream_of(x.device),
+            )
+        )
+
+
+@ExperimentalAPI(reason="Compact-B RowExpand; gfx950 HIP kernel, fixed-address metadata/lifetime contract.")
+def row_expand(
+    z: Tensor,
+    b: Tensor,
+    output: Tensor,
+    *,
+    b_offsets: Tensor,
+    b_strides: Tensor,
+    ranks: Tensor,
+    scales: Tensor,
+    segment_indptr: Tensor,
+    segment_slots: Tensor,
+    token_indices: Tensor,
+    slice_offsets: Tensor,
+    segment_count: Tensor,
+    blocks: int | None = None,
+    threads: int = 256,
+) -> None:
+    """Add compact B @ z to BF16 output, reusing B across <=16 token segments.
+
+    z is [tokens, slices * capacity], with each live slice packed at s*r.
+    B is flat; b_offsets are element offsets and b_strides are power-of-two
+    row widths in 1..64, at least the corresponding rank. B padding is zero.
+    Each segment has one slot and at most 16 distinct token indices. Tokens
+    occur at most once across active segments. slice_offsets partition output
+    columns; segment_count is a one-element int32 device vector.
+
+    FP32 dot products are scaled, rounded to BF16, added to the BF16 base,
+    and rounded again. Rank-zero and slot -1 segments leave output unchanged.
+    """
+    import torch
+
+    tensor(z, "z", 2, torch.bfloat16)
+    tensor(b, "b", 1, torch.bfloat16, z.device)
+    tensor(output, "output", 2, torch.bfloat16, z.device)
+    vector(ranks, "ranks", torch.int32, z.device)
+    nslots = ranks.numel()
+    for t, name, dtype in (
+        (b_offsets, "b_offsets", torch.int64),
+        (b_strides, "b_strides", torch.int32),
+        (scales, "scales", torch.float32),
+    ):
+        vector(t, name, dtype, z.device, nslots)
+    vector(segment_slots, "segment_slots", torch.int32, z.device)
+    vector(segment_indptr, "segment_indptr", torch.int32, z.device, segment_slots.numel() + 1)
+    vector(token_indices, "token_indices", torch.int32, z.device)
+    vector(slice_offsets, "slice_offsets", torch.int32, z.device)
+    vector(segment_count, "segment_count", torch.int32, z.device, 1)
+    slices = slice_offsets.numel() - 1
+    if (
+        nslots < 1
+        or not 1 <= slices <= 3
+        or z.shape[1] < slices
+        or z.shape[1] % slices
+        or output.shape[0] != z.shape[0]
+        or output.shape[1] < 1
+    ):
+        raise ValueError("invalid slots, slice count or activation/output shape")
+    if (
+        not z.is_contiguous()
+        or not b.is_contiguous()
+        or b.data_ptr() % 16
+        or output.stride(1) != 1
+        or output.stride(0) < output.shape[1]
+    ):
+        raise ValueError("expected contiguous z/aligned B and nonoverlapping output rows")
+    if blocks is not None and (type(blocks) is not int or not 1 <= blocks <= 65535):
+        raise ValueError("blocks must be in 1..65535")
+    if type(threads) is not int or threads not in (128, 256):
+        raise ValueError("threads must be 128 or 256")
+    column_blocks = (output.shape[1] + threads - 1) // threads
+    if segment_slots.numel() * column_blocks >= 2**31:
+        raise ValueError("segment work count must fit signed int32 indexing")
+    distinct_output(
+        output,
+        (z, b, b_offsets, b_strides, ranks, scales, segment_indptr, segment_slots, token_indices, slice_offsets, segment_count),
+    )
+    if z.shape[0] == 0:
+        return
+    require_arch(z.device)
+    lib = _lib.library()
+    with torch.cuda.device(z.device):
+        if blocks is None:
+            blocks = 2 * torch.cuda.get_device_properties(z.device).multi_processor_count
+        _lib.check(
+            lib.lf_row_expand(
+                z.data_ptr(),
+                b.data_ptr(),
+                b_offsets.data_ptr(),
+                b_strides.data_ptr(),
+                output.data_ptr(),
+                segment_indptr.data_ptr(),
+                segment_slots.data_ptr(),
+                token_indices.data_ptr(),
+                ranks.data_ptr(),
+                scales.data_ptr(),
+                slice_offsets.data_ptr(),
+                segment_count.data_ptr(),
+                z.shape[0],
+                output.shape[1],
+                output.stride(0),
+                slices,
+                z.shape[1] // slices,
+                blocks,
+                threads,
+                _lib.stream_of(z.device),
+            )
+        )
