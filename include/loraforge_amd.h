@@ -129,10 +129,15 @@ int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_
 
 /* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);
  * y [m, N] bf16 with row stride y_stride; bias bf16 [N] or NULL;
- * lora NULL for the base linear alone. */
+ * lora NULL for the base linear alone.
+ * flags: LF_EXACT_WEIGHTS makes the decode kernel multiply bf16_rne(code *
+ * scale) weights (the reference's dequantised W, bit for bit); by default it
+ * contracts bf16(code) and applies each fp32 block scale to the block's MFMA
+ * sum. The prefill GEMM always uses the exact weights. */
+#define LF_EXACT_WEIGHTS 1
 int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* weight,
                        const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                       void* workspace, int64_t workspace_bytes, void* stream);
+                       void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
 
 /* Reads the workspace status word written by the last call (0 = ok); for
  * tests and diagnostics only (synchronises the stream). */

@@ -18,6 +18,7 @@ LIBRARY = Path(__file__).resolve().parent / "_lib" / "libloraforge_amd.so"
 LF_OK = 0
 LF_EINVAL = 1
 LF_EHIP = 2
+LF_EXACT_WEIGHTS = 1
 ABI_VERSION = 1
 
 _lock = threading.Lock()
@@ -95,6 +96,7 @@ _PROTOTYPES = {
             c_int64,
             c_void_p,
             c_int64,
+            c_int32,
             c_void_p,
         ],
     ),

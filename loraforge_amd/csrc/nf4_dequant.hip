@@ -22,10 +22,7 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(const uint32_t* _
                                                                uint4* __restrict__ out, int64_t ndwords) {
   __shared__ float table[16];
   __shared__ float code2[kDouble ? 256 : 1];
-  if (threadIdx.x < 16) table[threadIdx.x] = code[threadIdx.x];
-  if constexpr (kDouble) code2[threadIdx.x] = src.code2[threadIdx.x];
-  __syncthreads();
-  const float offset = kDouble ? *src.offset : 0.0f;
+  // Packed bytes are requested first; the codebook is staged while they travel.
   const int64_t base = int64_t(blockIdx.x) * (kThreads * kSteps) + threadIdx.x;
   uint32_t words[kSteps];
 #pragma unroll
@@ -33,6 +30,10 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(const uint32_t* _
     const int64_t w = base + s * kThreads;
     words[s] = w < ndwords ? packed[w] : 0u;
   }
+  const float offset = kDouble ? *src.offset : 0.0f;
+  if (threadIdx.x < 16) table[threadIdx.x] = code[threadIdx.x];
+  if constexpr (kDouble) code2[threadIdx.x] = src.code2[threadIdx.x];
+  __syncthreads();
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int64_t w = base + s * kThreads;

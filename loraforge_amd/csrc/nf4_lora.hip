@@ -7,7 +7,7 @@ namespace lf {
 int decode_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_lora_decode(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                            const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                           void* workspace, int64_t workspace_bytes, void* stream);
+                           void* workspace, int64_t workspace_bytes, bool exact, void* stream);
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
@@ -24,8 +24,9 @@ extern "C" int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, i
 
 extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                                   const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
+                                  void* workspace, int64_t workspace_bytes, int32_t flags, void* stream) {
   LF_REQUIRE(w != nullptr, "weight descriptor required");
+  LF_REQUIRE((flags & ~LF_EXACT_WEIGHTS) == 0, "unknown flags");
   LF_REQUIRE(m >= 0 && m < (int64_t(1) << 31), "token count out of range");
   const int64_t n = w->n, k = w->k;
   LF_REQUIRE(n > 0 && k > 0 && n % 64 == 0 && k % 64 == 0, "weight shape must contain two positive multiples of 64");
@@ -46,7 +47,8 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
     LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
   }
   if (m <= lf::kDecodeMaxTokens)
-    return lf::launch_nf4_lora_decode(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, stream);
+    return lf::launch_nf4_lora_decode(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
+                                      (flags & LF_EXACT_WEIGHTS) != 0, stream);
   return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, stream);
 }
 

@@ -191,7 +191,9 @@ def _lora_struct(lora: LoraBatch, m: int, k: int, n: int, device):
 
 
 @ExperimentalAPI(reason="gfx950 fused NF4 + multi-LoRA linear; caller-owned device metadata.")
-def nf4_lora_linear(x, qweight, state, *, scales=None, bias=None, lora: LoraBatch | None = None, out=None, workspace=None):
+def nf4_lora_linear(
+    x, qweight, state, *, scales=None, bias=None, lora: LoraBatch | None = None, out=None, workspace=None, exact=False
+):
     """``y = bf16(x @ dequant(W)^T) (+bias)``, then the per-token LoRA delta.
 
     x: bf16 ``[..., K]`` with unit column stride. qweight: packed uint8
@@ -201,6 +203,12 @@ def nf4_lora_linear(x, qweight, state, *, scales=None, bias=None, lora: LoraBatc
     reconstructed inside the kernel. Returns bf16 ``[..., N]`` (``out`` if given).
     Launches on the current stream; the workspace (cached per device and
     stream unless passed) must not be shared by overlapping calls.
+
+    Decode batches (<= 64 tokens) contract ``bf16(code[nibble])`` on MFMA and
+    apply each fp32 block scale to the block's partial sum; ``exact=True``
+    instead multiplies the reference's dequantised weights
+    ``bf16_rne(code * scale)`` (bit-identical W, slower). Prefill always uses
+    the exact weights.
     """
     import torch
 
@@ -264,6 +272,7 @@ def nf4_lora_linear(x, qweight, state, *, scales=None, bias=None, lora: LoraBatc
                 y2.stride(0),
                 workspace.data_ptr(),
                 workspace.numel(),
+                _lib.LF_EXACT_WEIGHTS if exact else 0,
                 stream,
             )
         )

@@ -43,7 +43,7 @@ def test_validation_errors_without_device_work():
         _lib.check(lib.lf_row_shrink(*([ctypes.c_void_p(16)] * 5), 4, 64, 64, 5, 64, 16, None))
     w = _lib.NF4Weight(n=100, k=64)
     with pytest.raises(ValueError, match="multiples of 64"):
-        _lib.check(lib.lf_nf4_lora_linear(ctypes.c_void_p(16), 1, 64, ctypes.byref(w), None, None, ctypes.c_void_p(16), 64, None, 0, None))
+        _lib.check(lib.lf_nf4_lora_linear(ctypes.c_void_p(16), 1, 64, ctypes.byref(w), None, None, ctypes.c_void_p(16), 64, None, 0, 0, None))
 
 
 def test_workspace_size_is_host_arithmetic():

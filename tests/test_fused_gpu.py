@@ -73,6 +73,29 @@ def workspace_clean(device):
     assert decode_status(device=device) == 0
 
 
+@pytest.mark.parametrize("m", [1, 7, 16, 17, 40, 64])
+@pytest.mark.parametrize("dq", [False, True])
+def test_decode_exact_weights(m, dq, device):
+    """exact=True multiplies the reference's bf16(code * scale) weights."""
+    case = _cases.fused_case(m, 512, 1024, ranks=(16,) * 8, double_quant=dq, seed=200 + m)
+    x, q, st, lora, _ = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, lora=lora, exact=True)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+    workspace_clean(device)
+
+
+def test_decode_half_chunk_k(device):
+    """K % 128 == 64: the last chunk holds a single NF4 block."""
+    for m in (3, 20):
+        for exact in (False, True):
+            case = _cases.fused_case(m, 256, 320, ranks=(8, 4), double_quant=bool(m % 2), seed=m)
+            x, q, st, lora, _ = to_device(case, device)
+            y = nf4_lora_linear(x, q, st, lora=lora, exact=exact)
+            torch.cuda.synchronize()
+            close(bits(y), _cases.fused_expected(case))
+
+
 @pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 33, 48, 64])
 @pytest.mark.parametrize("dq", [False, True])
 def test_decode_batches(m, dq, device):
