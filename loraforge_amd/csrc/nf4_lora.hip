@@ -4,7 +4,7 @@
 #include "../../include/loraforge_amd.h"
 
 namespace lf {
-int decode_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
+int64_t decode_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_lora_decode(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                            const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                            void* workspace, int64_t workspace_bytes, bool exact, void* stream);

@@ -111,7 +111,40 @@ def _workspace(device, stream: int, size: int):
         return ws
 
 
-def _weight_struct(qweight, state, scales, n, k, device):
+def _decode_takes_nested(m: int, n: int, k: int, dq_block: int) -> bool:
+    """Whether the decode kernel rebuilds double-quant scales itself.
+
+    It stages the second-level scales of a workgroup's rows in a 256-entry
+    window and copies the uint8 codes four at a time, so it needs K % 256 == 0
+    and a window that covers the group (mirrors the plan in
+    ``csrc/nf4_lora_decode.hip``); other decode shapes take prepared fp32 scales.
+    """
+    if m > 64:
+        return True
+    tm = (m + 15) // 16
+    waves = 4 if tm <= 2 or n % 128 else 8
+    nseg = 4 if tm <= 2 else 2
+    rows, krange = 16 * waves, 256 * nseg
+    span = ((rows - 1) * (k // 64) + krange // 64) // dq_block + 2
+    return k % 256 == 0 and span <= 256
+
+
+def _prepared_scales(state):
+    """fp32 scales of a nested state, rebuilt once and kept on the state."""
+    from loraforge_amd.ops.nf4 import prepare_scales
+
+    cached = getattr(state, "_lf_prepared_scales", None)
+    if cached is None:
+        import torch
+
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("warm nf4_lora_linear with this weight before graph capture")
+        cached = prepare_scales(state)
+        state._lf_prepared_scales = cached
+    return cached
+
+
+def _weight_struct(qweight, state, scales, n, k, device, m=0):
     import torch
 
     code = state.code
@@ -125,6 +158,8 @@ def _weight_struct(qweight, state, scales, n, k, device):
     keep = [qweight, code]
     if scales is None and not state.nested:
         scales = state.absmax
+    if scales is None and not _decode_takes_nested(m, n, k, int(state.state2.blocksize)):
+        scales = _prepared_scales(state)
     if scales is not None:
         vector(scales.reshape(-1), "scales", torch.float32, device, n * k // 64)
         w.scales = scales.data_ptr()
@@ -246,7 +281,7 @@ def nf4_lora_linear(
     if m == 0:
         return out
     require_arch(device)
-    w, keep = _weight_struct(qweight, state, scales, n, k, device)
+    w, keep = _weight_struct(qweight, state, scales, n, k, device, m)
     lib = _lib.library()
     slices = lora.num_slices if lora is not None else 1
     max_rank = lora.max_rank if lora is not None else 1
