@@ -40,6 +40,23 @@ RANK = 16
 LAYERS = 64
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "decode_hbm_traffic.json"
+
+
+def measured_traffic(batch: int):
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    counter runs (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter
+    reads for a plain copy of known size), or None when not measured for this
+    batch."""
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    if int(rec.get("batch", -1)) != batch:
+        return None
+    return int(rec["traffic_bytes_per_launch"])
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -325,10 +342,12 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(head["frac"], 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.batch),
             "kernel": "nf4_lora_decode_kernel",
             "bytes_per_launch": head["bytes_per_call"],
             "us_per_launch": round(head["us_per_call"], 3),
+            "timing": "HIP events on the graph-replay stream over the timed calls (includes the graph's "
+            "inter-kernel dispatch gap; rocprofv3 kernel durations are in profiles/)",
         },
     }
     if not args.only:

@@ -62,10 +62,11 @@ namespace {
 
 constexpr int kSegK = 256;      // k per pipeline segment: 4 NF4 blocks
 constexpr int kShrinkK = 1024;  // k per lane pass of the shrink dot products (2 x 8 per lane)
-constexpr int kCtrlBytes = 256;
+constexpr int kCtrlBytes = 512;
 constexpr int kSpinLimit = 1 << 22;
 constexpr int kMaxUnits = 256;
-enum Ctrl { kZDone = 0, kDone = 1, kStatus = 2 };
+// Control words: groups finished, status, and one z-ready counter per distinct slot.
+enum Ctrl { kDone = 1, kStatus = 2, kSlotDone = 64 };
 
 struct DecodeParams {
   const uint16_t* x;
@@ -465,36 +466,25 @@ __device__ __forceinline__ void compute_segment(f32x4 (&acc)[S::kTM], const floa
 }
 
 struct LoraShared;
-struct ShrinkStep;
-struct ExpandPre;
 template <class S>
 __device__ void lora_prologue(const DecodeParams& p, LoraShared* ls, int wave, int lane);
-template <class S>
-__device__ void lora_prefetch(const DecodeParams& p, const LoraShared* ls, int split, int row0, int wave, int lane,
-                              ShrinkStep& sst, bool& have_shrink, ExpandPre& ep, bool& have_expand);
 
 // After segment 0 the LoRA metadata is gathered (its slot copy was issued
 // first, so the segment-0 wait covers it); later segments keep arriving.
 template <class S, int SEG, bool kDouble, bool kLora, bool kExact>
 __device__ __forceinline__ void run_segments(const DecodeParams& p, f32x4 (&acc)[S::kTM], const float* table,
                                              const uint32_t* ptl, int wave, int lane, int row0, int kbase,
-                                             float offset, LoraShared* ls, int split, ShrinkStep& sst,
-                                             bool& have_shrink, ExpandPre& ep, bool& have_expand) {
+                                             float offset, LoraShared* ls) {
   wait_vm_lgkm<(S::kNSeg - 1 - SEG) * S::kDmaSeg>();  // this wave's copies up to segment SEG landed
   barrier_only();                                      // ... and every other wave's
   if constexpr (SEG == 0 && kDouble) {
     rebuild_dq_scales<S>(p, row0, kbase, offset);
     lds_sync();
   }
-  // Every copy has landed once the last segment's wait returns: LoRA operand
-  // loads issued from here on cannot delay a copy wait (vmcnt is in order).
-  if constexpr (SEG + 1 == S::kNSeg && kLora)
-    lora_prefetch<S>(p, ls, split, row0, wave, lane, sst, have_shrink, ep, have_expand);
   compute_segment<S, SEG, kExact>(acc, table, ptl, wave, lane, (p.k >> 6) - (kbase >> 6));
   if constexpr (SEG == 0 && kLora) lora_prologue<S>(p, ls, wave, lane);
   if constexpr (SEG + 1 < S::kNSeg)
-    run_segments<S, SEG + 1, kDouble, kLora, kExact>(p, acc, table, ptl, wave, lane, row0, kbase, offset, ls, split,
-                                                     sst, have_shrink, ep, have_expand);
+    run_segments<S, SEG + 1, kDouble, kLora, kExact>(p, acc, table, ptl, wave, lane, row0, kbase, offset, ls);
 }
 
 // ---------------------------------------------------------------------------
@@ -598,63 +588,16 @@ __device__ void lora_prologue(const DecodeParams& p, LoraShared* ls, int wave, i
 }
 
 // Shrink units owned by this group: unit u = (distinct d = u / kz, k-slice u % kz).
-// Rows s*r + j of A_g against every token of slot g, fp32 partial sums over the
-// slice. One step covers 4 rows per wave, 4 tokens and 1024 k (two 16-byte
-// loads per lane and operand).
-struct ShrinkStep {
-  uint4 a[4][2];
-  uint4 xv[4][2];
-};
-
+// z partial [tokens of slot g][rows s*r + j of A_g] over the slice on MFMA:
+// x rows of the slot's tokens as the A operand, A_g rows as the B operand,
+// 16 x 16 tiles; the waves split the slice's 32-k steps (8 steps of loads in
+// flight per wave) and their tiles are summed through LDS. A finished unit
+// bumps its slot's z-ready counter (the owners of that slot wait for kz).
 template <class S>
-__device__ __forceinline__ void shrink_load(const DecodeParams& p, const LoraShared* ls, const uint16_t* abase,
-                                            int rows, int j0, int tb, int t1, int kc, int ke, int lane,
-                                            ShrinkStep& st) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int kk = kc + h * 512 + lane * 8;
-    const bool ok = kk < ke;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = j0 + i * S::kWaves;
-      st.a[i][h] = ok && j < rows ? *reinterpret_cast<const uint4*>(abase + int64_t(j) * p.k + kk)
-                                  : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int tt = tb + c;
-      st.xv[c][h] = ok && tt < t1 ? *reinterpret_cast<const uint4*>(p.x + int64_t(ls->dtok[tt]) * p.x_stride + kk)
-                                  : make_uint4(0, 0, 0, 0);
-    }
-  }
-}
-
-// The first step of this group's first unit, requested early (right after the
-// slot metadata) so that it arrives while the base contraction runs.
-template <class S>
-__device__ __forceinline__ bool shrink_prefetch(const DecodeParams& p, const LoraShared* ls, int wave, int lane,
-                                                ShrinkStep& st) {
-  const int u = blockIdx.x;
-  if (u >= ls->nd * p.kz) return false;
-  const int d = u / p.kz;
-  const int ks = u - d * p.kz;
-  const int r = ls->drank[d];
-  if (r == 0) return false;
-  const int kb = ks * p.kz_len;
-  shrink_load<S>(p, ls, p.a_store + ls->daoff[d], p.slices * r, wave, ls->dptr[d], ls->dptr[d + 1], kb,
-                 min(p.k, kb + p.kz_len), lane, st);
-  return true;
-}
-
-// Returns the number of units handled (each counts once toward kZDone).
-template <class S>
-__device__ int shrink_units(const DecodeParams& p, const LoraShared* ls, int wave, int lane, const ShrinkStep& pre,
-                            bool have_pre) {
+__device__ void shrink_units(const DecodeParams& p, const LoraShared* ls, int wave, int lane, float* red) {
   const int units = ls->nd * p.kz;
-  int handled = 0;
-  bool first = have_pre;
+  const int kg = lane >> 4;
   for (int u = blockIdx.x; u < units; u += gridDim.x) {
-    ++handled;
     const int d = u / p.kz;
     const int ks = u - d * p.kz;
     const int r = ls->drank[d];
@@ -662,52 +605,66 @@ __device__ int shrink_units(const DecodeParams& p, const LoraShared* ls, int wav
     const int rows = p.slices * r;
     const int kb = ks * p.kz_len;
     const int ke = min(p.k, kb + p.kz_len);
+    const int nsteps = (ke - kb) >> 5;
     const int t0 = ls->dptr[d], t1 = ls->dptr[d + 1];
     const uint16_t* abase = p.a_store + ls->daoff[d];
-    for (int tb = t0; tb < t1; tb += 4) {
-      for (int j0 = wave; j0 < rows; j0 += 4 * S::kWaves) {
-        float acc[4][4];
+    for (int tt0 = t0; tt0 < t1; tt0 += 16) {
+      const int ti = tt0 + (lane & 15);
+      const int tok = ls->dtok[ti < t1 ? ti : t0];  // padded rows repeat a token; never stored
+      const uint16_t* xrow = p.x + int64_t(tok) * p.x_stride + kb + 8 * kg;
+      for (int j0 = 0; j0 < rows; j0 += 16) {
+        const int jr = j0 + (lane & 15) < rows ? j0 + (lane & 15) : j0;
+        const uint16_t* arow = abase + int64_t(jr) * p.k + kb + 8 * kg;
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        for (int st0 = wave; st0 < nsteps; st0 += 8 * S::kWaves) {
+          uint4 xa[8], aa[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[i][c] = 0.f;
-        for (int kc = kb; kc < ke; kc += kShrinkK) {
-          ShrinkStep st;
-          if (first) {
-            st = pre;
-            first = false;
-          } else {
-            shrink_load<S>(p, ls, abase, rows, j0, tb, t1, kc, ke, lane, st);
+          for (int i = 0; i < 8; ++i) {
+            const int st = st0 + i * S::kWaves;
+            const bool ok = st < nsteps;
+            xa[i] = ok ? *reinterpret_cast<const uint4*>(xrow + 32 * st) : make_uint4(0, 0, 0, 0);
+            aa[i] = ok ? *reinterpret_cast<const uint4*>(arow + 32 * st) : make_uint4(0, 0, 0, 0);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              acc[i][c] = dot8(st.a[i][1], st.xv[c][1], dot8(st.a[i][0], st.xv[c][0], acc[i][c]));
+          for (int i = 0; i < 8; ++i) c = mfma16(as_bf16x8(xa[i]), as_bf16x8(aa[i]), c);
         }
+        *reinterpret_cast<f32x4*>(red + (wave * 64 + lane) * 4) = c;
+        __syncthreads();
+        if (wave == 0) {
+          f32x4 sum = c;
+          for (int w = 1; w < S::kWaves; ++w) {
+            const f32x4 o = *reinterpret_cast<const f32x4*>(red + (w * 64 + lane) * 4);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const float s = wave_sum(acc[i][c]);
-            const int j = j0 + i * S::kWaves;
-            const int tt = tb + c;
-            if (lane == 0 && j < rows && tt < t1)
-              shared_store(p.zpart + (int64_t(ks) * p.m + ls->dtok[tt]) * p.zw + j, s);
+            for (int e = 0; e < 4; ++e) sum[e] += o[e];
           }
+          const int j = j0 + (lane & 15);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int tj = tt0 + 4 * kg + e;
+            if (tj < t1 && j < rows)
+              shared_store(p.zpart + (int64_t(ks) * p.m + ls->dtok[tj]) * p.zw + j, sum[e]);
+          }
+        }
+        __syncthreads();  // this tile's z partials stored
       }
     }
+    if (threadIdx.x == 0) counter_add(p.ctrl + kSlotDone + d, 1);
   }
-  return handled;
 }
 
-// Bounded wait on a device counter (thread 0); a timeout records a status
-// instead of hanging the launch.
-__device__ void wait_counter(const DecodeParams& p, const int* counter, int target) {
+// Bounded wait (thread 0) until the z-ready counter of every owned slot
+// (d = split, split + splits, ...) reaches kz. Each poll issues all counter
+// loads together, so one device-coherent round trip checks every slot; a
+// timeout records a status instead of hanging the launch.
+__device__ void wait_owned_slots(const DecodeParams& p, const LoraShared* ls, int split) {
   if (threadIdx.x == 0) {
     int spins = 0;
-    while (counter_load(counter) < target) {
-      __builtin_amdgcn_s_sleep(8);  // every group polls the same word: keep the traffic low
+    for (;;) {
+      bool done = true;
+      for (int d = split; d < ls->nd; d += p.splits)
+        if (ls->drank[d] > 0 && counter_load(p.ctrl + kSlotDone + d) < p.kz) done = false;
+      if (done) break;
+      __builtin_amdgcn_s_sleep(4);
       if (++spins > kSpinLimit) {
         counter_store(p.ctrl + kStatus, 1);
         break;
@@ -825,17 +782,6 @@ __device__ void lora_expand(const DecodeParams& p, const LoraShared* ls, int spl
   }
 }
 
-template <class S>
-__device__ void lora_prefetch(const DecodeParams& p, const LoraShared* ls, int split, int row0, int wave, int lane,
-                              ShrinkStep& sst, bool& have_shrink, ExpandPre& ep, bool& have_expand) {
-  have_shrink = shrink_prefetch<S>(p, ls, wave, lane, sst);
-  have_expand = split < ls->nd && slice_hits_tile(ls, 0, row0 + wave * 16);
-  if (have_expand) {
-    int dd[8];
-    expand_frags(p, ls, split, 0, 0, row0 + wave * 16 + (lane & 15), lane >> 4, ep.bf, dd);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
@@ -873,24 +819,26 @@ __global__ __launch_bounds__(WAVES * 64) void nf4_lora_decode_kernel(DecodeParam
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) acc[tm] = (f32x4){0.f, 0.f, 0.f, 0.f};
   const uint32_t* ptl = pt + (lane % S::kCopies);
-  ShrinkStep sst;
-  ExpandPre ep;
-  bool have_shrink = false, have_expand = false;
-  run_segments<S, 0, kDouble, kLora, kExact>(p, acc, table, ptl, wave, lane, row0, kbase, offset, ls, split, sst,
-                                             have_shrink, ep, have_expand);
+  run_segments<S, 0, kDouble, kLora, kExact>(p, acc, table, ptl, wave, lane, row0, kbase, offset, ls);
   __syncthreads();  // every copy consumed: LDS buffers may be reused
 
   f32x4 dacc[TM];
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) dacc[tm] = (f32x4){0.f, 0.f, 0.f, 0.f};
   if constexpr (kLora) {
-    const int handled = shrink_units<S>(p, ls, wave, lane, sst, have_shrink);
-    __syncthreads();  // this group's z partials stored
-    if (threadIdx.x == 0 && handled) counter_add(p.ctrl + kZDone, handled);
+    // The W segment-0 buffer is dead here: it holds the shrink's cross-wave tiles.
+    shrink_units<S>(p, ls, wave, lane, reinterpret_cast<float*>(lds_region<16, S::kWSeg>()));
     bool owns = false;
     for (int d = split; d < ls->nd; d += p.splits) owns |= ls->drank[d] > 0;
     if (owns) {
-      wait_counter(p, p.ctrl + kZDone, ls->nd * p.kz);
+      // B fragments of the first owned batch are requested before the z wait.
+      ExpandPre ep;
+      const bool have_expand = slice_hits_tile(ls, 0, row0 + wave * 16);
+      if (have_expand) {
+        int dd[8];
+        expand_frags(p, ls, split, 0, 0, row0 + wave * 16 + (lane & 15), lane >> 4, ep.bf, dd);
+      }
+      wait_owned_slots(p, ls, split);
       // z is staged in a dead segment buffer (x of segment 0, or W of segment 0 when x is small).
       char* zl_bytes;
       if constexpr (S::kXSeg >= S::kZlBytes) zl_bytes = lds_region<32, S::kXSeg>();
@@ -985,8 +933,8 @@ __global__ __launch_bounds__(WAVES * 64) void nf4_lora_decode_kernel(DecodeParam
   if constexpr (kLora) {
     if (threadIdx.x == 0) {
       const int done = counter_add(p.ctrl + kDone, 1);
-      if (done == int(gridDim.x) - 1) {  // every group is past its z wait: reset for the next call
-        counter_store(p.ctrl + kZDone, 0);
+      if (done == int(gridDim.x) - 1) {  // every group is past its z waits: reset for the next call
+        for (int d = 0; d < ls->nd; ++d) counter_store(p.ctrl + kSlotDone + d, 0);
         counter_store(p.ctrl + kDone, 0);
       }
     }
