@@ -59,20 +59,36 @@ struct PrefillParams {
 
 __device__ __forceinline__ int swz(int row, int unit) { return row * 8 + (unit ^ (row & 7)); }
 
-// Distinct live slots of tokens [t0, t0 + count), written to list[0..], count in list[kMaxList].
+// Live slot of each token of [t0, t0 + count) (rank 0 or above 64: base
+// only, -1), loaded by one thread per token, and the distinct live slots in
+// order of first use: list[0 .. list[kMaxList]). Wave 0 extracts them with
+// one ballot per distinct slot; the slots of a prefill tile are few.
 constexpr int kMaxList = 64;
-__device__ void distinct_slots(const PrefillParams& p, int t0, int count, int* list) {
-  if (threadIdx.x == 0) {
+__device__ void live_slots(const PrefillParams& p, int t0, int count, int* tslot, int* list) {
+  for (int t = threadIdx.x; t < kThreads; t += blockDim.x) {
+    int g = t < count ? p.token_slots[t0 + t] : -1;
+    const int r = g >= 0 ? p.ranks[g] : 0;
+    if (r <= 0 || r > kZSlice) g = -1;  // rank 0 / contract violation: base only
+    tslot[t] = g;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
     int nd = 0;
-    for (int t = 0; t < count; ++t) {
-      const int g = p.token_slots[t0 + t];
-      const int r = g >= 0 ? p.ranks[g] : 0;
-      if (r <= 0 || r > kZSlice) continue;  // rank 0 / contract violation: base only
-      bool seen = false;
-      for (int i = 0; i < nd; ++i) seen |= list[i] == g;
-      if (!seen && nd < kMaxList) list[nd++] = g;
+    for (int c = 0; c < count; c += 64) {
+      const int g = c + lane < count ? tslot[c + lane] : -1;
+      uint64_t left = __ballot(g >= 0);
+      while (left) {
+        const int gf = __builtin_amdgcn_readlane(g, __builtin_ctzll(left));
+        left &= ~__ballot(g == gf);
+        const int known = lane < nd ? list[lane] : -2;
+        if (__ballot(known == gf) == 0 && nd < kMaxList) {
+          if (lane == 0) list[nd] = gf;
+          ++nd;
+        }
+      }
     }
-    list[kMaxList] = nd;
+    if (lane == 0) list[kMaxList] = nd;
   }
   __syncthreads();
 }
@@ -82,11 +98,13 @@ __device__ void distinct_slots(const PrefillParams& p, int t0, int count, int* l
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void prefill_shrink_kernel(PrefillParams p) {
   __shared__ int list[kMaxList + 1];
-  __shared__ int tslot[16];
+  __shared__ int tslot[kThreads];
+  __shared__ int trank[16];
   const int t0 = blockIdx.x * 16;
   const int count = min(16, p.m - t0);
-  if (threadIdx.x < 16) tslot[threadIdx.x] = threadIdx.x < count ? p.token_slots[t0 + threadIdx.x] : -1;
-  distinct_slots(p, t0, count, list);
+  live_slots(p, t0, count, tslot, list);
+  if (threadIdx.x < 16) trank[threadIdx.x] = tslot[threadIdx.x] >= 0 ? p.ranks[tslot[threadIdx.x]] : 0;
+  __syncthreads();
   const int nd = list[kMaxList];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -96,11 +114,8 @@ __global__ __launch_bounds__(kThreads) void prefill_shrink_kernel(PrefillParams 
   for (int i = threadIdx.x; i < count * zw; i += kThreads) {
     const int t = i / zw;
     const int col = i - t * zw;
-    const int g = tslot[t];
-    if (g >= 0) {
-      const int r = p.ranks[g];
-      if (r > 0 && r <= kZSlice && (col % kZSlice) >= r) p.zpad[int64_t(t0 + t) * zw + col] = 0;
-    }
+    const int r = trank[t];
+    if (r > 0 && (col % kZSlice) >= r) p.zpad[int64_t(t0 + t) * zw + col] = 0;
   }
   for (int d = 0; d < nd; ++d) {
     const int g = list[d];
@@ -112,12 +127,20 @@ __global__ __launch_bounds__(kThreads) void prefill_shrink_kernel(PrefillParams 
     for (int ct = wave; ct * 16 < rows; ct += 4) {
       const int j = ct * 16 + (lane & 15);
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int kc = 0; kc < p.k; kc += 32) {
-        const int kb = kc + gq * 8;
-        uint4 xv = make_uint4(0, 0, 0, 0), av = make_uint4(0, 0, 0, 0);
-        if (mine) xv = *reinterpret_cast<const uint4*>(p.x + int64_t(t0 + tok) * p.x_stride + kb);
-        if (j < rows) av = *reinterpret_cast<const uint4*>(ag + int64_t(j) * p.k + kb);
-        acc = mfma16(as_bf16x8(xv), as_bf16x8(av), acc);
+      // K is a multiple of 64; 8 steps of 32 k have their loads in flight together.
+      const uint16_t* xrow = p.x + int64_t(t0 + (mine ? tok : 0)) * p.x_stride + gq * 8;
+      const uint16_t* arow = ag + int64_t(j < rows ? j : 0) * p.k + gq * 8;
+      for (int kc = 0; kc < p.k; kc += 8 * 32) {
+        uint4 xv[8], av[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int kk = kc + 32 * i;
+          const bool ok = kk < p.k;
+          xv[i] = ok && mine ? *reinterpret_cast<const uint4*>(xrow + kk) : make_uint4(0, 0, 0, 0);
+          av[i] = ok && j < rows ? *reinterpret_cast<const uint4*>(arow + kk) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = mfma16(as_bf16x8(xv[i]), as_bf16x8(av[i]), acc);
       }
       // acc[e] = z[token 4*gq + e][column j]
       if (j < rows) {
@@ -244,8 +267,7 @@ __global__ __launch_bounds__(kThreads) void prefill_gemm_kernel(PrefillParams p)
       }
   }
   if constexpr (kLora) {
-    tslot[tid] = m0 + tid < p.m ? p.token_slots[m0 + tid] : -1;
-    distinct_slots(p, m0, min(kBM, p.m - m0), list);
+    live_slots(p, m0, min(kBM, p.m - m0), tslot, list);
     const int nd = list[kMaxList];
     const int zw = p.slices * kZSlice;
     const int wn0 = n0 + wn * 64;
@@ -256,11 +278,20 @@ __global__ __launch_bounds__(kThreads) void prefill_gemm_kernel(PrefillParams p)
       const float scale = p.lscales[g];
       const uint16_t* bg = p.b_store + p.b_offsets[g];
       const int ksteps = (r + 31) / 32;
+      // Bit 4*i + e: the lane's output row wm*128 + 16i + 4gq + e is routed to g.
+      uint32_t rows_of_g = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rows_of_g |= uint32_t(tslot[wm * 128 + i * 16 + 4 * gq + e] == g) << (4 * i + e);
       for (int s = 0; s < p.slices; ++s) {
         const int lo = p.slice_offsets[s];
         const int hi = p.slice_offsets[s + 1];
         if (hi <= wn0 || lo >= wn0 + 64) continue;
-        // B fragments for the wave's 4 column blocks, up to 2 k-steps (r <= 64).
+        // B fragments (the wave's 4 column blocks, up to 2 k-steps: r <= 64)
+        // and z fragments (its 8 token blocks) are all requested before the
+        // first MFMA: one memory round trip per slot and slice.
         bf16x8 bfr[4][2];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -272,29 +303,31 @@ __global__ __launch_bounds__(kThreads) void prefill_gemm_kernel(PrefillParams p)
             bfr[j][st] = as_bf16x8(v);
           }
         }
+        bf16x8 zf[8][2];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int tl = wm * 128 + i * 16;
-          bf16x8 zf[2];
-          const int arow = tl + lr;
+          const int arow = wm * 128 + i * 16 + lr;
           const bool amine = tslot[arow] == g;
 #pragma unroll
           for (int st = 0; st < 2; ++st) {
             uint4 v = make_uint4(0, 0, 0, 0);
             if (amine && st < ksteps)
               v = *reinterpret_cast<const uint4*>(p.zpad + int64_t(m0 + arow) * zw + s * kZSlice + st * 32 + gq * 8);
-            zf[st] = as_bf16x8(v);
+            zf[i][st] = as_bf16x8(v);
           }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
-            dacc = mfma16(zf[0], bfr[j][0], dacc);
-            if (ksteps > 1) dacc = mfma16(zf[1], bfr[j][1], dacc);
+            dacc = mfma16(zf[i][0], bfr[j][0], dacc);
+            if (ksteps > 1) dacc = mfma16(zf[i][1], bfr[j][1], dacc);
             const int n = wn0 + j * 16 + lr;
             const bool col = n >= lo && n < hi;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              if (col && tslot[tl + 4 * gq + e] == g)
+              if (col && ((rows_of_g >> (4 * i + e)) & 1u))
                 acc[i][j][e] = round_bf16(acc[i][j][e] + round_bf16(dacc[e] * scale));
             }
           }
