@@ -168,7 +168,7 @@ __device__ __forceinline__ uint4 load_b8(const uint16_t* brow, int kk, int br) {
 }
 
 template <bool kDouble, bool kLora>
-__global__ __launch_bounds__(kThreads) void prefill_gemm_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(PrefillParams p) {
   __shared__ uint4 xs[kBM * 8];
   __shared__ uint4 ws[kBN * 8];
   __shared__ float table[16];
@@ -288,10 +288,12 @@ __global__ __launch_bounds__(kThreads) void prefill_gemm_kernel(PrefillParams p)
       for (int s = 0; s < p.slices; ++s) {
         const int lo = p.slice_offsets[s];
         const int hi = p.slice_offsets[s + 1];
-        if (hi <= wn0 || lo >= wn0 + 64) continue;
+        // Every wave takes part in the z staging (it holds barriers); only
+        // waves whose 64 columns meet the slice do MFMA work.
+        const bool hit = !(hi <= wn0 || lo >= wn0 + 64);
         // B fragments (the wave's 4 column blocks, up to 2 k-steps: r <= 64)
-        // and z fragments (its 8 token blocks) are all requested before the
-        // first MFMA: one memory round trip per slot and slice.
+        // are requested first; the tile's z rows of this slice are staged in
+        // the (idle) x buffer, [token][64 ranks] bf16 with the x swizzle.
         bf16x8 bfr[4][2];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -299,30 +301,32 @@ __global__ __launch_bounds__(kThreads) void prefill_gemm_kernel(PrefillParams p)
 #pragma unroll
           for (int st = 0; st < 2; ++st) {
             uint4 v = make_uint4(0, 0, 0, 0);
-            if (st < ksteps && n < p.n) v = load_b8(bg + int64_t(n) * br, st * 32 + gq * 8, br);
+            if (hit && st < ksteps && n < p.n) v = load_b8(bg + int64_t(n) * br, st * 32 + gq * 8, br);
             bfr[j][st] = as_bf16x8(v);
           }
         }
-        bf16x8 zf[8][2];
+        __syncthreads();  // previous users of xs are done
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int row = (tid >> 3) + 32 * q;
+          const int unit = tid & 7;
+          uint4 v = make_uint4(0, 0, 0, 0);
+          if (tslot[row] == g && unit < 4 * ksteps)
+            v = *reinterpret_cast<const uint4*>(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + unit * 8);
+          xs[swz(row, unit)] = v;
+        }
+        __syncthreads();
+        if (!hit) continue;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int arow = wm * 128 + i * 16 + lr;
-          const bool amine = tslot[arow] == g;
-#pragma unroll
-          for (int st = 0; st < 2; ++st) {
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (amine && st < ksteps)
-              v = *reinterpret_cast<const uint4*>(p.zpad + int64_t(m0 + arow) * zw + s * kZSlice + st * 32 + gq * 8);
-            zf[i][st] = as_bf16x8(v);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
+          const bf16x8 z0 = as_bf16x8(xs[swz(arow, gq)]);
+          const bf16x8 z1 = as_bf16x8(xs[swz(arow, 4 + gq)]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
-            dacc = mfma16(zf[i][0], bfr[j][0], dacc);
-            if (ksteps > 1) dacc = mfma16(zf[i][1], bfr[j][1], dacc);
+            dacc = mfma16(z0, bfr[j][0], dacc);
+            if (ksteps > 1) dacc = mfma16(z1, bfr[j][1], dacc);
             const int n = wn0 + j * 16 + lr;
             const bool col = n >= lo && n < hi;
 #pragma unroll
