@@ -122,9 +122,10 @@ typedef struct lf_lora {
 } lf_lora;
 
 /* Bytes of device workspace lf_nf4_lora_linear needs for this problem. The
- * first 256 bytes hold counters that must be zero before the first call;
- * every completed call leaves them zero again. Calls that share one
- * workspace must not overlap in time. */
+ * first 64 KiB hold control counters that must be zero before the first
+ * call; every completed call leaves them zero again (decode and prefill
+ * calls may share one workspace). Calls that share one workspace must not
+ * overlap in time. */
 int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices, int32_t max_rank);
 
 /* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);

@@ -993,8 +993,8 @@ struct Layout {
 Layout workspace_layout(int64_t m, int64_t n, int64_t k, int slices, int max_rank) {
   const Plan pl = make_plan(m, n, k);
   Layout l;
-  l.tile_count = kCtrlBytes;
-  l.zpart = align256(l.tile_count + 4 * (n / pl.rows + 1));
+  l.tile_count = kCtrlBytes;  // one counter per column group, inside the control header
+  l.zpart = kWorkspaceHeader;
   l.dpart = align256(l.zpart + 4 * int64_t(pl.kz) * m * slices * max_rank);
   const int64_t split_bytes = pl.splits > 1 ? 4 * m * n : 0;
   l.part = align256(l.dpart + split_bytes);
@@ -1041,6 +1041,7 @@ int launch_nf4_lora_decode(const uint16_t* x, int64_t m, int64_t x_stride, const
   LF_REQUIRE(aligned16(workspace), "workspace must be 16-byte aligned");
   const Plan pl = make_plan(m, n, k);
   LF_REQUIRE(n % pl.rows == 0, "output width must be a multiple of %d", pl.rows);
+  LF_REQUIRE(kCtrlBytes + 4 * (n / pl.rows) <= kWorkspaceHeader, "output width too large for the decode path");
   if (!w->scales) {
     // In-kernel double-quant staging covers groups whose second-level scales
     // fit a 256-entry window; other shapes take prepared fp32 scales.

@@ -14,9 +14,11 @@
 //     in LDS) to exact bf16 and written to LDS; four waves (2 x 2) each own
 //     128 x 64 outputs as 8 x 4 fragments of v_mfma_f32_16x16x32_bf16.
 //     LDS rows are 128 B with a 16-byte-unit XOR swizzle (unit ^ row % 8).
-//     Epilogue: round, bias, then for every distinct slot in the tile a
-//     second MFMA pass zpad x B_g^T gives the LoRA delta, applied with the
-//     reference's two bf16 roundings to the rows routed to that slot.
+//     Epilogue: round, bias, then per slice the tile's z rows are staged in
+//     LDS once and, for every distinct slot in the tile, a second MFMA pass
+//     z x B_g^T over the 16-row blocks holding its tokens gives the LoRA
+//     delta, applied with the reference's two bf16 roundings to the rows
+//     routed to that slot.
 //  Tile order puts M-tile b % mtiles on consecutive block ids, so with 8
 //  M-tiles each XCD (block id % 8) keeps one 2 MiB x panel in its L2.
 #include "nf4_common.h"
@@ -62,8 +64,9 @@ __device__ __forceinline__ int swz(int row, int unit) { return row * 8 + (unit ^
 // Live slot of each token of [t0, t0 + count) (rank 0 or above 64: base
 // only, -1), loaded by one thread per token, and the distinct live slots in
 // order of first use: list[0 .. list[kMaxList]). Wave 0 extracts them with
-// one ballot per distinct slot; the slots of a prefill tile are few.
-constexpr int kMaxList = 64;
+// one ballot per distinct slot of each 64-token chunk; a slot already listed
+// (checked 64 entries per ballot) is not added again.
+constexpr int kMaxList = kBM;  // a tile routes to at most one slot per token
 __device__ void live_slots(const PrefillParams& p, int t0, int count, int* tslot, int* list) {
   for (int t = threadIdx.x; t < kThreads; t += blockDim.x) {
     int g = t < count ? p.token_slots[t0 + t] : -1;
@@ -81,8 +84,9 @@ __device__ void live_slots(const PrefillParams& p, int t0, int count, int* tslot
       while (left) {
         const int gf = __builtin_amdgcn_readlane(g, __builtin_ctzll(left));
         left &= ~__ballot(g == gf);
-        const int known = lane < nd ? list[lane] : -2;
-        if (__ballot(known == gf) == 0 && nd < kMaxList) {
+        bool seen = false;
+        for (int b = 0; b < nd && !seen; b += 64) seen = __ballot(b + lane < nd && list[b + lane] == gf) != 0;
+        if (!seen) {
           if (lane == 0) list[nd] = gf;
           ++nd;
         }
@@ -173,7 +177,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(PrefillParams
   __shared__ uint4 ws[kBN * 8];
   __shared__ float table[16];
   __shared__ float code2[kDouble ? 256 : 1];
-  __shared__ int tslot[kBM];
+  __shared__ __attribute__((aligned(16))) int tslot[kBM];
   __shared__ int list[kMaxList + 1];
   const int tid = threadIdx.x;
   if (tid < 16) table[tid] = p.code[tid];
@@ -271,68 +275,79 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(PrefillParams
     const int nd = list[kMaxList];
     const int zw = p.slices * kZSlice;
     const int wn0 = n0 + wn * 64;
-    for (int d = 0; d < nd; ++d) {
+    // Per distinct slot metadata in the (idle) W buffer.
+    int* mrank = reinterpret_cast<int*>(ws);
+    int* mstride = mrank + kMaxList;
+    float* mscale = reinterpret_cast<float*>(mstride + kMaxList);
+    int64_t* mboff = reinterpret_cast<int64_t*>(mscale + kMaxList);
+    static_assert(sizeof(ws) >= kMaxList * (3 * 4 + 8), "slot metadata fits the W buffer");
+    for (int d = tid; d < nd; d += kThreads) {
       const int g = list[d];
-      const int r = p.ranks[g];
-      const int br = p.b_strides[g];
-      const float scale = p.lscales[g];
-      const uint16_t* bg = p.b_store + p.b_offsets[g];
-      const int ksteps = (r + 31) / 32;
-      // Bit 4*i + e: the lane's output row wm*128 + 16i + 4gq + e is routed to g.
-      uint32_t rows_of_g = 0;
+      mrank[d] = p.ranks[g];
+      mstride[d] = p.b_strides[g];
+      mscale[d] = p.lscales[g];
+      mboff[d] = p.b_offsets[g];
+    }
+    for (int s = 0; s < p.slices; ++s) {
+      const int lo = p.slice_offsets[s];
+      const int hi = p.slice_offsets[s + 1];
+      // Every token's z row of this slice (zeros past its rank; zeros for
+      // base-only tokens) is staged once in the x buffer, [token][64] bf16
+      // with the x swizzle; each slot's pass reads the rows it needs.
+      __syncthreads();  // previous users of xs (and the metadata stores) are done
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int q = 0; q < 8; ++q) {
+        const int row = (tid >> 3) + 32 * q;
+        const int unit = tid & 7;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (tslot[row] >= 0) v = *reinterpret_cast<const uint4*>(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + unit * 8);
+        xs[swz(row, unit)] = v;
+      }
+      __syncthreads();
+      if (hi <= wn0 || lo >= wn0 + 64) continue;  // this wave's 64 columns miss the slice
+      for (int d = 0; d < nd; ++d) {
+        const int g = list[d];
+        // Bit 4i + e: the lane's row wm*128 + 16i + 4gq + e is routed to g.
+        uint32_t mine = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          rows_of_g |= uint32_t(tslot[wm * 128 + i * 16 + 4 * gq + e] == g) << (4 * i + e);
-      for (int s = 0; s < p.slices; ++s) {
-        const int lo = p.slice_offsets[s];
-        const int hi = p.slice_offsets[s + 1];
-        // Every wave takes part in the z staging (it holds barriers); only
-        // waves whose 64 columns meet the slice do MFMA work.
-        const bool hit = !(hi <= wn0 || lo >= wn0 + 64);
-        // B fragments (the wave's 4 column blocks, up to 2 k-steps: r <= 64)
-        // are requested first; the tile's z rows of this slice are staged in
-        // the (idle) x buffer, [token][64 ranks] bf16 with the x swizzle.
-        bf16x8 bfr[4][2];
+        for (int i = 0; i < 8; ++i) {
+          const int4 ts = *reinterpret_cast<const int4*>(tslot + wm * 128 + i * 16 + 4 * gq);
+          mine |= (uint32_t(ts.x == g) | uint32_t(ts.y == g) << 1 | uint32_t(ts.z == g) << 2 | uint32_t(ts.w == g) << 3)
+                  << (4 * i);
+        }
+        if (__ballot(mine != 0) == 0) continue;  // none of this wave's 128 rows takes g
+        // B fragments of slot d: 4 column blocks, up to 2 k-steps (r <= 64).
+        const int r = mrank[d];
+        const int br = mstride[d];
+        const uint16_t* bg = p.b_store + mboff[d];
+        bf16x8 b0[4], b1[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int n = wn0 + j * 16 + lr;
-#pragma unroll
-          for (int st = 0; st < 2; ++st) {
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (hit && st < ksteps && n < p.n) v = load_b8(bg + int64_t(n) * br, st * 32 + gq * 8, br);
-            bfr[j][st] = as_bf16x8(v);
-          }
+          uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+          if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, gq * 8, br);
+          if (r > 32 && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + gq * 8, br);
+          b0[j] = as_bf16x8(v0);
+          b1[j] = as_bf16x8(v1);
         }
-        __syncthreads();  // previous users of xs are done
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int row = (tid >> 3) + 32 * q;
-          const int unit = tid & 7;
-          uint4 v = make_uint4(0, 0, 0, 0);
-          if (tslot[row] == g && unit < 4 * ksteps)
-            v = *reinterpret_cast<const uint4*>(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + unit * 8);
-          xs[swz(row, unit)] = v;
-        }
-        __syncthreads();
-        if (!hit) continue;
+        const bool two = r > 32;
+        const float scale = mscale[d];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
+          if (__ballot((mine >> (4 * i)) & 15u) == 0) continue;  // no row of this 16-row block takes g
           const int arow = wm * 128 + i * 16 + lr;
           const bf16x8 z0 = as_bf16x8(xs[swz(arow, gq)]);
           const bf16x8 z1 = as_bf16x8(xs[swz(arow, 4 + gq)]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
-            dacc = mfma16(z0, bfr[j][0], dacc);
-            if (ksteps > 1) dacc = mfma16(z1, bfr[j][1], dacc);
+            dacc = mfma16(z0, b0[j], dacc);
+            if (two) dacc = mfma16(z1, b1[j], dacc);
             const int n = wn0 + j * 16 + lr;
             const bool col = n >= lo && n < hi;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              if (col && ((rows_of_g >> (4 * i + e)) & 1u))
-                acc[i][j][e] = round_bf16(acc[i][j][e] + round_bf16(dacc[e] * scale));
+              if (col && ((mine >> (4 * i + e)) & 1u)) acc[i][j][e] = round_bf16(acc[i][j][e] + round_bf16(dacc[e] * scale));
             }
           }
         }
@@ -356,7 +371,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(PrefillParams
 }  // namespace
 
 int64_t prefill_workspace_bytes(int64_t m, int64_t, int64_t, int slices, int) {
-  return (m * slices * kZSlice * 2 + 255) / 256 * 256 + 256;
+  return kWorkspaceHeader + (m * slices * kZSlice * 2 + 255) / 256 * 256 + 256;
 }
 
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
@@ -393,7 +408,7 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.lscales = lora->scales;
     p.token_slots = lora->token_slots;
     p.slice_offsets = lora->slice_offsets;
-    p.zpad = static_cast<uint16_t*>(workspace);
+    p.zpad = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + kWorkspaceHeader);  // after the decode counters
     hipLaunchKernelGGL(prefill_shrink_kernel, dim3(unsigned((m + 15) / 16)), dim3(kThreads), 0, s, p);
     LF_HIP(hipGetLastError());
   }
