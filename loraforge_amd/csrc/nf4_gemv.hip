@@ -1,0 +1,841 @@
+// Decode NF4 linear (M <= 64 tokens) without split-K.
+//
+// Reference chain (integrations/_sglang_nf4_linear.py:116-129):
+//   y = bf16(x @ dequant(W)^T) (+ bias, rounded again).
+//
+// Each workgroup owns R = 16 * RT output rows and a tile of up to 32 tokens
+// over the whole K, so no partial sums cross workgroups. Its eight waves split
+// the NF4 blocks of K between them; each wave streams its own blocks through
+// a private LDS ring (W bytes, x rows, block scales) filled by direct
+// global -> LDS copies, waits only on its own copy counter, and contracts
+// each block on bf16 MFMA (16 tokens x 16 rows x 32 k). Two waves per SIMD
+// keep two such chains in flight. The eight partial tiles are summed through
+// LDS once at the end.
+//
+// Per-CU traffic is R * K / 2 bytes of W plus T * K * 2 bytes of x; the x
+// rows are shared by every workgroup and come from L2. With N = 4096:
+// M <= 16 uses 16 rows x 16 tokens (256 workgroups), M <= 32 16 x 32, and
+// M <= 64 32 x 32 (128 row groups x 2 token tiles, both on one XCD so W is
+// read from HBM once).
+#include <algorithm>
+
+#include "nf4_common.h"
+#include "../../include/loraforge_amd.h"
+
+namespace lf {
+namespace {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kCopies = 16;  // pair-table copies (lane l reads copy l % 16)
+
+// RT: 16-row output tiles; XR: staged token rows (2, 8, 16 or 32).
+template <int RT, int XR>
+struct Tile {
+  static constexpr int kRT = RT;
+  static constexpr int kR = 16 * RT;
+  static constexpr int kXR = XR;
+  static constexpr int kTT = XR > 16 ? 2 : 1;                  // 16-token MFMA tiles
+  static constexpr int kSB = (RT == 1 && XR <= 16) ? 2 : 1;    // NF4 blocks per stage
+  static constexpr int kWBytes = 1024;                          // one copy: kR * kSB * 32 bytes used
+  static constexpr int kXBytes = XR * kSB * 128 < 1024 ? 1024 : XR * kSB * 128;
+  static constexpr int kXDma = kXBytes / 1024;
+  static constexpr int kScBytes = 256;  // one dword copy: kR * kSB scales used
+  static constexpr int kStage = kWBytes + kXBytes + kScBytes;
+  static constexpr int kDma = 2 + kXDma;  // copies per stage
+  static constexpr int kDepth = 3;
+  static_assert(kR * kSB * 32 <= kWBytes && kR * kSB <= 64, "stage sizes");
+  static_assert(kDma * (kDepth - 1) < 64, "vmcnt range");
+};
+
+struct GemvParams {
+  const uint16_t* x;
+  int64_t x_stride;
+  int m;
+  const uint8_t* q;
+  const float* scales;
+  const float* code;
+  int n;
+  int k;
+  const uint16_t* bias;
+  uint16_t* y;
+  int64_t y_stride;
+  int row_groups;  // n / R
+  // LoRA (kLora variants only).
+  const uint16_t* a_store;
+  const int64_t* a_offsets;
+  const uint16_t* b_store;
+  const int64_t* b_offsets;
+  const int32_t* b_strides;
+  const int32_t* ranks;
+  const float* lscales;
+  const int32_t* token_slots;
+  const int32_t* slice_offsets;
+  int slices;
+  int max_rank;
+  int zw;         // z row width: slices * max_rank
+  int units;      // shrink units: m * kz (unit u = token u / kz, k-slice u % kz)
+  int kz;         // k-slices per token
+  int kz_len;     // k per slice (multiple of 64)
+  int consumers;  // workgroups that read each unit: row_groups
+  int producers;  // workgroups b < producers make units b, b + producers, ...
+  int* status;    // set to 1 when a bounded wait times out
+  int* counters;  // [units] published-unit counters, zero between calls
+  float* zp;      // [units][zw] shrink partial sums
+};
+
+constexpr int kSpinLimit = 1 << 20;
+
+template <class T>
+__device__ __forceinline__ T sload(const T* base, int idx) {
+  typedef const __attribute__((address_space(4))) T* ConstPtr;
+  return ((ConstPtr)base)[idx];
+}
+
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0xF << 8) | (7 << 4));  // vmcnt(N) only
+}
+
+// vmcnt(n) for n = c * kDma, c < kDepth (runtime c).
+template <class TL>
+__device__ __forceinline__ void wait_stages(int c) {
+  switch (c) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<TL::kDma>(); break;
+    case 2: wait_vm<2 * TL::kDma>(); break;
+    case 3: wait_vm<3 * TL::kDma>(); break;
+    case 4: wait_vm<4 * TL::kDma>(); break;
+    case 5: wait_vm<(TL::kDepth > 5 ? 5 : 0) * TL::kDma>(); break;
+    case 6: wait_vm<(TL::kDepth > 6 ? 6 : 0) * TL::kDma>(); break;
+    default: wait_vm<(TL::kDepth > 7 ? 7 : 0) * TL::kDma>(); break;
+  }
+}
+
+__device__ __forceinline__ void copy16(const void* src, char* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void copy4(const void* src, char* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+// LDS reads the compiler does not track: the ring is written by direct copies
+// whose completion each wave checks itself (vmcnt), so no compiler wait may
+// be attached to these reads. Results are valid after lds_wait().
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16x8 vec_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ u32x2 lds_read64(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ u32x4 lds_read128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ float lds_read32f(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// lgkmcnt(0), then every value read by the untracked LDS reads is tied to
+// the wait so that no use can be scheduled above it.
+template <class T>
+__device__ __forceinline__ void tie(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
+template <int kC>
+__device__ __forceinline__ uint4 codes_dword(uint32_t d, const uint32_t* ptl) {
+  uint4 r;
+  r.x = ptl[(d & 0xffu) * kC];
+  r.y = ptl[__builtin_amdgcn_ubfe(d, 8, 8) * kC];
+  r.z = ptl[__builtin_amdgcn_ubfe(d, 16, 8) * kC];
+  r.w = ptl[(d >> 24) * kC];
+  return r;
+}
+
+// Lane (n = l & 15, g = l >> 4) holds W[row n][16g .. 16g + 16) of an NF4
+// block (8 bytes) and x[token][same k]; MFMA step j covers k = 16g + 8j .. +8.
+// Default: bf16(code) contracted, the fp32 block scale applied to the block
+// sum; exact: bf16_rne(code * scale) weights (the reference's dequantised W).
+// Ring fragments of one stage for this lane: W bytes (8 per block and row
+// tile), block scales, and x fragments (2 x 16 bytes per block and token tile).
+template <class TL>
+struct Frags {
+  u32x2 q[TL::kSB][TL::kRT];
+  float sc[TL::kSB][TL::kRT];
+  u32x4 xf[TL::kSB][TL::kTT][2];
+};
+
+template <class TL>
+__device__ __forceinline__ void read_frags(Frags<TL>& f, uint32_t wbase, int n, int g) {
+  const uint32_t xbase = wbase + TL::kWBytes;
+  const uint32_t sbase = xbase + TL::kXBytes;
+#pragma unroll
+  for (int b = 0; b < TL::kSB; ++b) {
+#pragma unroll
+    for (int r = 0; r < TL::kRT; ++r) {
+      const int row = r * 16 + n;
+      f.q[b][r] = lds_read64(wbase + (b * TL::kR + row) * 32 + 8 * g);
+      f.sc[b][r] = lds_read32f(sbase + (b * TL::kR + row) * 4);
+    }
+#pragma unroll
+    for (int t = 0; t < TL::kTT; ++t) {
+      const int xr = (t * 16 + n) % TL::kXR;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        f.xf[b][t][j] = lds_read128(xbase + (xr * TL::kSB + b) * 128 + (((2 * g + j) ^ (xr & 7)) << 4));
+    }
+  }
+}
+
+// Waits for the untracked ring reads and ties their results to the wait.
+template <class TL>
+__device__ __forceinline__ void settle(Frags<TL>& f) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int b = 0; b < TL::kSB; ++b) {
+#pragma unroll
+    for (int r = 0; r < TL::kRT; ++r) {
+      tie(f.q[b][r]);
+      tie(f.sc[b][r]);
+    }
+#pragma unroll
+    for (int t = 0; t < TL::kTT; ++t) {
+      tie(f.xf[b][t][0]);
+      tie(f.xf[b][t][1]);
+    }
+  }
+}
+
+// Decodes every W fragment of the stage first (all codebook lookups in
+// flight together), then runs the MFMAs. Blocks past the wave's range get
+// scale 0.
+template <class TL, bool kExact>
+__device__ __forceinline__ void contract(const Frags<TL>& f, int kb, int kend, f32x4 (&acc)[TL::kRT][TL::kTT],
+                                         const float* table, const uint32_t* ptl) {
+  uint4 w[TL::kSB][TL::kRT][2];
+  float sc[TL::kSB][TL::kRT];
+#pragma unroll
+  for (int b = 0; b < TL::kSB; ++b)
+#pragma unroll
+    for (int r = 0; r < TL::kRT; ++r) {
+      sc[b][r] = kb + b < kend ? f.sc[b][r] : 0.f;
+      if constexpr (kExact) {
+        w[b][r][0] = decode_dword(f.q[b][r].x, sc[b][r], table);
+        w[b][r][1] = decode_dword(f.q[b][r].y, sc[b][r], table);
+      } else {
+        w[b][r][0] = codes_dword<kCopies>(f.q[b][r].x, ptl);
+        w[b][r][1] = codes_dword<kCopies>(f.q[b][r].y, ptl);
+      }
+    }
+#pragma unroll
+  for (int b = 0; b < TL::kSB; ++b)
+#pragma unroll
+    for (int r = 0; r < TL::kRT; ++r)
+#pragma unroll
+      for (int t = 0; t < TL::kTT; ++t) {
+        if constexpr (kExact) {
+          acc[r][t] = mfma16(vec_bf16x8(f.xf[b][t][0]), as_bf16x8(w[b][r][0]), acc[r][t]);
+          acc[r][t] = mfma16(vec_bf16x8(f.xf[b][t][1]), as_bf16x8(w[b][r][1]), acc[r][t]);
+        } else {
+          const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+          f32x4 d = mfma16(vec_bf16x8(f.xf[b][t][0]), as_bf16x8(w[b][r][0]), zero);
+          d = mfma16(vec_bf16x8(f.xf[b][t][1]), as_bf16x8(w[b][r][1]), d);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[r][t][e] = __builtin_fmaf(sc[b][r], d[e], acc[r][t][e]);
+        }
+      }
+}
+
+
+// ---------------------------------------------------------------------------
+// LoRA wave (the last wave of every workgroup when LoRA is on).
+//
+// Shrink: unit u = (token t = u / kz, k-slice u % kz) is computed at the
+// start of workgroup u % producers: zp[u][j] = sum over the slice of x[t][k] *
+// A_g[j][k] for the slices * r rows of the token's adapter (MFMA, the token
+// row repeated across the 16 MFMA rows), stored with device-scope stores;
+// once they complete, counters[u] += consumers.
+// Expand: every workgroup waits until the units of its tile's tokens are
+// published, sums their k-slices (z = bf16(sum)), subtracts 1 from each
+// counter it read (so all counters are back to zero when the launch ends),
+// and computes bf16(scale_g * sum_j z[t][s r + j] * B_g[n][j]) for its
+// outputs on VALU, written in the layout of the base partial tiles.
+// Units are produced before any wait, by the first min(grid, CUs)
+// workgroups (one per CU), so every wait is for a workgroup that is already
+// running.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int counter_load(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_add(int* p, int v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void shared_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float shared_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// All waves of a producing workgroup share its units at the start, while
+// their first weight copies are in flight: wave w takes the 32-k MFMA steps
+// w, w + 8, ... of the unit's slice, the partial rows meet in red[wave][j],
+// and the LoRA wave (publisher) sums, stores and publishes them. Every
+// branch here is uniform over the workgroup (barriers inside).
+__device__ void produce_units(const GemvParams& p, float* red, int wave, int lane, bool publisher) {
+  if (blockIdx.x >= unsigned(p.producers)) return;
+  for (int u = blockIdx.x; u < p.units; u += p.producers) {
+    const int t = u / p.kz;
+    const int ks = u - t * p.kz;
+    const int g = sload(p.token_slots, t);
+    if (g < 0) continue;
+    const int r = sload(p.ranks, g);
+    if (r <= 0 || r > p.max_rank) continue;  // base only
+    const int64_t aoff = sload(p.a_offsets, g);
+    const int rows = p.slices * r;
+    const int kb = ks * p.kz_len;
+    const int steps = (min(p.k, kb + p.kz_len) - kb) >> 5;
+    const int jn = lane & 15;
+    const int kg = lane >> 4;
+    const uint16_t* xrow = p.x + int64_t(t) * p.x_stride + kb + 8 * kg;
+    for (int j0 = 0; j0 < rows; j0 += 16) {
+      const int j = j0 + jn;
+      const uint16_t* arow = p.a_store + aoff + int64_t(j < rows ? j : rows - 1) * p.k + kb + 8 * kg;
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      for (int st0 = wave; st0 < steps; st0 += 8 * kWaves) {
+        uint4 xv[8], av[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int st = st0 + i * kWaves;
+          const bool ok = st < steps;
+          xv[i] = ok ? *reinterpret_cast<const uint4*>(xrow + 32 * st) : make_uint4(0, 0, 0, 0);
+          av[i] = ok ? *reinterpret_cast<const uint4*>(arow + 32 * st) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c = mfma16(as_bf16x8(xv[i]), as_bf16x8(av[i]), c);
+      }
+      // Row 0 of C (lanes 0..15, element 0) holds this wave's partial of z[j0 + lane].
+      if (kg == 0) red[wave * 192 + j0 + jn] = c[0];
+    }
+    __syncthreads();
+    float v[3];
+    if (publisher) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const int jj = q * 64 + lane;
+        v[q] = 0.f;
+        if (jj < rows)
+          for (int w = 0; w < kWaves; ++w) v[q] += red[w * 192 + jj];
+      }
+    }
+    __syncthreads();  // red is free again
+    if (publisher) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        if (q * 64 + lane < rows) shared_store(p.zp + int64_t(u) * p.zw + q * 64 + lane, v[q]);
+      wait_vm<0>();  // partial stores complete
+      if (lane == 0) counter_add(p.counters + u, p.consumers);
+    }
+  }
+}
+
+// Token metadata of the tile, one entry per tile token (g = -1: base only).
+struct TileMeta {
+  int g[32];
+  int r[32];
+  int stride[32];
+  float scale[32];
+  int64_t boff[32];
+};
+
+// Up to 8 B values (16 bytes) of B row n of an adapter (offset boff, row
+// stride st, rank r) from rank j0; zeros past the rank.
+__device__ __forceinline__ uint4 load_b8(const GemvParams& p, int64_t boff, int st, int r, int n, int j0) {
+  const uint16_t* bp = p.b_store + boff + int64_t(n) * st + j0;
+  if (j0 >= r) return make_uint4(0, 0, 0, 0);
+  if ((st & 7) == 0) return *reinterpret_cast<const uint4*>(bp);  // stride >= 8: 16-byte rows
+  uint32_t h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = j0 + e < r ? bp[e] : 0u;
+  return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+}
+
+__device__ __forceinline__ float dot8(const uint4& b, const uint4& z, float acc) {
+  const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+  const uint32_t zw[4] = {z.x, z.y, z.z, z.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc = __builtin_fmaf(bf16_lo(zw[q]), bf16_lo(bw[q]), acc);
+    acc = __builtin_fmaf(bf16_hi(zw[q]), bf16_hi(bw[q]), acc);
+  }
+  return acc;
+}
+
+template <class TL>
+__device__ void lora_wave(const GemvParams& p, char* lds, int row0, int t0, int mt, int lane) {
+  constexpr int RT = TL::kRT;
+  constexpr int TT = TL::kTT;
+  constexpr int kTiles = RT * TT;
+  constexpr int kCols = TL::kR / 2;  // output columns per lane
+  float* dtile = reinterpret_cast<float*>(lds);
+  TileMeta* tm = reinterpret_cast<TileMeta*>(lds + kTiles * 1024);
+  // z, slice padded: [tile token][slice][64] bf16, zero past the rank.
+  uint16_t* zl = reinterpret_cast<uint16_t*>(lds + kTiles * 1024 + 1024);
+  float* stage = reinterpret_cast<float*>(lds + kTiles * 1024 + 1024 + TL::kXR * 192 * 2);
+
+  // Tile token metadata.
+  int g = -1, r = 0, stride = 1;
+  float scale = 0.f;
+  int64_t boff = 0;
+  if (lane < mt) {
+    g = p.token_slots[t0 + lane];
+    if (g >= 0) {
+      r = p.ranks[g];
+      if (r <= 0 || r > p.max_rank) {
+        g = -1;
+        r = 0;
+      } else {
+        stride = p.b_strides[g];
+        scale = p.lscales[g];
+        boff = p.b_offsets[g];
+      }
+    }
+  }
+  if (lane < 32) {
+    tm->g[lane] = g;
+    tm->r[lane] = r;
+    tm->stride[lane] = stride;
+    tm->scale[lane] = scale;
+    tm->boff[lane] = boff;
+  }
+  int bounds[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) bounds[b] = b <= p.slices ? sload(p.slice_offsets, b) : 0;
+
+  // Expand operands, one token per lane (i = lane % 32) over half of the
+  // tile's columns (lane / 32): ranks 0..15 of the first 8 columns' B rows
+  // are requested before the wait for z.
+  const int i = lane & 31;
+  const int half = lane >> 5;
+  const bool live = i < mt && tm->g[i] >= 0;
+  const int ri = tm->r[i];
+  const int st = tm->stride[i];
+  const int64_t bo = tm->boff[i];
+  const float sc = tm->scale[i];
+  constexpr int kPre = kCols < 8 ? kCols : 8;
+  uint4 bv[kPre][2];
+#pragma unroll
+  for (int q = 0; q < kPre; ++q) {
+    const int n = row0 + half * kCols + q;
+    bv[q][0] = live ? load_b8(p, bo, st, ri, n, 0) : make_uint4(0, 0, 0, 0);
+    bv[q][1] = live ? load_b8(p, bo, st, ri, n, 8) : make_uint4(0, 0, 0, 0);
+  }
+
+  // Wait until every unit of the tile's routed tokens is published.
+  const int pairs = mt * p.kz;
+  for (int spins = 0;; ++spins) {
+    bool ready = true;
+    for (int c0 = 0; c0 < pairs; c0 += 64) {
+      const int pr = c0 + lane;
+      const int i = pr / p.kz;
+      const bool need = pr < pairs && tm->g[i] >= 0;
+      const int v = need ? counter_load(p.counters + t0 * p.kz + pr) : 1;
+      ready = ready && __all(v > 0);
+    }
+    if (ready) break;
+    if (spins > kSpinLimit) {
+      if (lane == 0) __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  // The tile's partials are one contiguous block zp[t0 * kz .. (t0 + mt) * kz)
+  // of zw values each (units of base-only tokens hold stale values and are
+  // never used): up to 16 loads per lane at a time into LDS, then z[i][j] =
+  // bf16(sum over the kz <= 16 slices).
+  for (int e = lane; e < TL::kXR * 192 / 8; e += 64) reinterpret_cast<uint4*>(zl)[e] = make_uint4(0, 0, 0, 0);
+  // Whole tokens per batch: per_token <= 1024 (the plan keeps
+  // tile tokens x zw x kz <= 1024 whenever kz > 1).
+  const int per_token = p.kz * p.zw;
+  const int tpb = 1024 / per_token;
+  const float* block = p.zp + int64_t(t0) * per_token;
+  for (int i0 = 0; i0 < mt; i0 += tpb) {
+    const int e0 = i0 * per_token;
+    const int count = min(tpb, mt - i0) * per_token;
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int e = q * 64 + lane;
+      v[q] = e < count ? shared_load(block + e0 + e) : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) stage[q * 64 + lane] = v[q];
+    for (int o = lane; o < count / p.kz; o += 64) {
+      const int il = o / p.zw;  // token within the batch
+      const int j = o - il * p.zw;
+      const float* src = stage + il * per_token + j;
+      float z = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks)
+        if (ks < p.kz) z += src[ks * p.zw];
+      const int i = i0 + il;
+      const int ri = tm->r[i];
+      const int s = ri > 0 ? j / ri : 3;
+      if (tm->g[i] >= 0 && s < p.slices) zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(z));
+    }
+  }
+  for (int c0 = 0; c0 < pairs; c0 += 64) {
+    const int pr = c0 + lane;
+    const int i = pr / p.kz;
+    if (pr < pairs && tm->g[i] >= 0) counter_add(p.counters + t0 * p.kz + pr, -1);
+  }
+
+  // Expand: delta = bf16(scale * sum_j z[i][s*r + j] * B_g[n][j]), eight
+  // columns and 16 ranks of B at a time (the first batch is already here).
+  {
+    float acc[kCols];
+#pragma unroll
+    for (int q = 0; q < kCols; ++q) acc[q] = 0.f;
+#pragma unroll
+    for (int c0 = 0; c0 < kCols; c0 += kPre) {
+      for (int j0 = 0; j0 < p.max_rank; j0 += 16) {
+        if (c0 > 0 || j0 > 0) {
+#pragma unroll
+          for (int q = 0; q < kPre; ++q) {
+            const int n = row0 + half * kCols + c0 + q;
+            bv[q][0] = live ? load_b8(p, bo, st, ri, n, j0) : make_uint4(0, 0, 0, 0);
+            bv[q][1] = live ? load_b8(p, bo, st, ri, n, j0 + 8) : make_uint4(0, 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kPre; ++q) {
+          const int n = row0 + half * kCols + c0 + q;
+          int s = 0;
+          while (s + 1 < p.slices && n >= bounds[s + 1]) ++s;
+          const uint4* zr = reinterpret_cast<const uint4*>(zl + (i * 3 + s) * 64 + j0);
+          if (live && j0 < ri) {
+            acc[c0 + q] = dot8(bv[q][0], zr[0], acc[c0 + q]);
+            acc[c0 + q] = dot8(bv[q][1], zr[1], acc[c0 + q]);
+          }
+        }
+      }
+    }
+    // Into the base tile layout: tile (rt, tt), lane (col % 16) + 16 * (tok % 16 / 4), element tok % 4.
+    if (i < 16 * TT) {
+#pragma unroll
+      for (int q = 0; q < kCols; ++q) {
+        const int col = half * kCols + q;
+        const int c = (col / 16) * TT + i / 16;
+        const int l = (col & 15) + 16 * ((i & 15) >> 2);
+        dtile[(c * 64 + l) * 4 + (i & 3)] = live ? round_bf16(acc[q] * sc) : 0.f;
+      }
+    }
+  }
+}
+
+// Copies of one stage (kSB blocks starting at block kb) into a ring slot.
+// W: position p -> block p / (2R), row (p / 2) % R, 16-byte half p % 2, so a
+// block's rows are 32 contiguous bytes each. x: position p -> token row
+// p / (8 kSB), block (p / 8) % kSB, unit slot p % 8 holding 16-byte unit
+// (p % 8) ^ (row & 7) (conflict-free fragment reads). Scales: position
+// p -> block p / R, row p % R. Positions past the stage and blocks past the
+// wave's range read valid addresses of block kb (their scale is zeroed when
+// used).
+template <class TL>
+__device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int row0, int t0, int mt, int kb,
+                                            int kend, int lane) {
+  const int nblk = p.k >> 6;
+  {
+    const int b = lane / (2 * TL::kR);
+    const int r = (lane >> 1) % TL::kR;
+    const int blk = (lane < 2 * TL::kR * TL::kSB && kb + b < kend) ? kb + b : kb;
+    copy16(p.q + int64_t(row0 + r) * (p.k >> 1) + blk * 32 + (lane & 1) * 16, slot);
+  }
+#pragma unroll
+  for (int d = 0; d < TL::kXDma; ++d) {
+    const int pos = d * 64 + lane;
+    int row = pos / (8 * TL::kSB);
+    const int b = (pos / 8) % TL::kSB;
+    const int u = (pos & 7) ^ (row & 7);
+    int blk = kb + b < kend ? kb + b : kb;
+    if (row >= TL::kXR) row = 0;
+    const int tok = t0 + (row < mt ? row : mt - 1);
+    copy16(p.x + int64_t(tok) * p.x_stride + blk * 64 + u * 8, slot + TL::kWBytes + d * 1024);
+  }
+  {
+    const int b = lane / TL::kR;
+    const int r = lane % TL::kR;
+    const int blk = (lane < TL::kR * TL::kSB && kb + b < kend) ? kb + b : kb;
+    copy4(p.scales + int64_t(row0 + r) * nblk + (blk < nblk ? blk : 0), slot + TL::kWBytes + TL::kXBytes);
+  }
+}
+
+template <int RT, int XR, bool kExact, bool kLora>
+__global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
+  using TL = Tile<RT, XR>;
+  constexpr int TT = TL::kTT;
+  constexpr int D = TL::kDepth;
+  constexpr int kBase = kLora ? kWaves - 1 : kWaves;  // waves on the base contraction
+  // The LoRA wave keeps its delta tiles, tile metadata, z and a 4 KiB partial
+  // staging area in its own ring region plus 6 KiB.
+  static_assert(!kLora || RT * TT * 1024 + 1024 + XR * 192 * 2 + 4096 <= D * TL::kStage + 6144, "LoRA wave LDS");
+  __shared__ __attribute__((aligned(16))) char ring[kWaves * D * TL::kStage + (kLora ? 6144 : 0)];
+  __shared__ float table[16];
+  __shared__ __attribute__((aligned(16))) uint32_t pt[kExact ? 4 : 256 * kCopies];
+  __shared__ float red[kLora ? kWaves * 192 : 1];
+
+  const int rg = blockIdx.x % p.row_groups;
+  const int tile = blockIdx.x / p.row_groups;
+  const int row0 = rg * TL::kR;
+  const int t0 = tile * 32;
+  const int mt = min(32, p.m - t0);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int nblk = p.k >> 6;
+  const int kb0 = wave < kBase ? nblk * wave / kBase : 0;
+  const int kend = wave < kBase ? nblk * (wave + 1) / kBase : 0;
+  const int nst = (kend - kb0 + TL::kSB - 1) / TL::kSB;
+  char* myring = ring + wave * D * TL::kStage;
+
+  // Codebook through scalar loads (no vector load may wait behind the copies).
+  float cb[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) cb[i] = sload(p.code, i);
+
+#pragma unroll
+  for (int s = 0; s < D; ++s)
+    if (s < nst) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, kb0 + s * TL::kSB, kend, lane);
+
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) table[i] = cb[i];
+  }
+  if constexpr (!kExact) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    barrier_only();
+    if (threadIdx.x < 256) {
+      const uint32_t v = pack_bf16x2(table[threadIdx.x >> 4], table[threadIdx.x & 15]);
+      uint4* dst = reinterpret_cast<uint4*>(pt + threadIdx.x * kCopies);
+#pragma unroll
+      for (int c = 0; c < kCopies / 4; ++c) dst[c] = make_uint4(v, v, v, v);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  barrier_only();
+  const uint32_t* ptl = pt + (lane % kCopies);
+  if constexpr (kLora) produce_units(p, red, wave, lane, wave == kBase);
+
+  f32x4 acc[RT][TT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const uint32_t ring_base = lds_addr(myring);
+  // Fragments of stage s + 1 are read from the ring while stage s is decoded
+  // and contracted; the slot of stage s is refilled as soon as its fragments
+  // are in registers.
+  Frags<TL> cur, nxt;
+  if (nst > 0) {
+    wait_stages<TL>(min(D - 1, nst - 1));
+    read_frags<TL>(cur, ring_base, n, g);
+    settle(cur);
+  }
+  for (int s = 0; s < nst; ++s) {
+    const bool more = s + 1 < nst;
+    if (more) {
+      wait_stages<TL>(min(D - 2, nst - 2 - s));
+      read_frags<TL>(nxt, ring_base + ((s + 1) % D) * TL::kStage, n, g);
+    }
+    if (s + D < nst)
+      issue_stage<TL>(p, myring + (s % D) * TL::kStage, row0, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
+    const int kb = kb0 + s * TL::kSB;
+    contract<TL, kExact>(cur, kb, kend, acc, table, ptl);
+    if (more) {
+      settle(nxt);
+      cur = nxt;
+    }
+  }
+
+  // Sum the waves' partial tiles: wave w writes its tiles into its own ring
+  // (all of its copies have landed), then tile c = wave is summed by wave c.
+  // The LoRA wave writes the rounded, scaled expand deltas in the same layout.
+  if (kLora && wave == kBase) {
+    lora_wave<TL>(p, myring, row0, t0, mt, lane);
+  } else {
+    f32x4* red = reinterpret_cast<f32x4*>(myring);
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) red[(r * TT + t) * 64 + lane] = acc[r][t];
+  }
+  __syncthreads();
+  constexpr int kTiles = RT * TT;
+  if (wave < kTiles) {
+    const int r = wave / TT;
+    const int t = wave % TT;
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kBase; ++w) {
+      const f32x4 v = reinterpret_cast<const f32x4*>(ring + w * D * TL::kStage)[wave * 64 + lane];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[e] += v[e];
+    }
+    f32x4 delta = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kLora) delta = reinterpret_cast<const f32x4*>(ring + kBase * D * TL::kStage)[wave * 64 + lane];
+    const int col = row0 + r * 16 + n;
+    const float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tok = t0 + t * 16 + 4 * g + e;
+      if (tok - t0 < mt) {
+        float v = round_bf16(sum[e]);
+        if (p.bias) v = round_bf16(v + bias);
+        if constexpr (kLora) v += delta[e];  // zero for base-only tokens; the store rounds
+        p.y[int64_t(tok) * p.y_stride + col] = uint16_t(f32_to_bf16(v));
+      }
+    }
+  }
+}
+
+template <int RT, int XR, bool kLora>
+void launch_exact(bool exact, dim3 grid, hipStream_t s, const GemvParams& p) {
+  if (exact) hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, true, kLora>), grid, dim3(kThreads), 0, s, p);
+  else hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, kLora>), grid, dim3(kThreads), 0, s, p);
+}
+
+template <int RT, int XR>
+void launch_tile(bool exact, bool lora, dim3 grid, hipStream_t s, const GemvParams& p) {
+  if (lora) launch_exact<RT, XR, true>(exact, grid, s, p);
+  else launch_exact<RT, XR, false>(exact, grid, s, p);
+}
+
+constexpr int64_t kCounterOffset = 256;  // counters follow the status words in the control header
+
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+struct GemvPlan {
+  int rows;
+  int row_groups;
+  int grid;
+  int kz;
+  int kz_len;
+  int units;
+  int producers;
+};
+
+// Shrink units: m tokens x kz k-slices, kz chosen so that m * kz is about
+// min(grid, CUs) (one unit per producing workgroup when m allows) and a
+// consumer's partial reads fit one batch.
+GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
+  GemvPlan pl;
+  pl.rows = m > 32 ? 32 : 16;
+  pl.row_groups = int(n / pl.rows);
+  pl.grid = pl.row_groups * int((m + 31) / 32);
+  const int64_t cap = std::min<int64_t>(pl.grid, cus);
+  const int64_t nblk = k / 64;
+  // A consumer reads tile tokens x zw x kz partials: keep that to one
+  // 1024-value batch where the shape allows, and at most half of the
+  // workgroups producing (production delays their contraction).
+  const int64_t tile_tokens = std::min<int64_t>(m, 32);
+  const int64_t kz = std::max<int64_t>(
+      1, std::min<int64_t>({nblk, cap / (2 * m), 16, 1024 / std::max<int64_t>(1, tile_tokens * zw)}));
+  pl.kz_len = int((nblk + kz - 1) / kz) * 64;
+  pl.kz = int((k + pl.kz_len - 1) / pl.kz_len);
+  pl.units = int(m) * pl.kz;
+  pl.producers = int(cap);
+  return pl;
+}
+
+}  // namespace
+
+int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank) {
+  const GemvPlan pl = gemv_plan(m, n, k, 1 << 20, slices * max_rank);  // upper bound over CU counts
+  return kWorkspaceHeader + (int64_t(pl.units) * slices * max_rank * 4 + 255) / 256 * 256;
+}
+
+// Fused NF4 + multi-LoRA linear for 1..64 tokens with fp32 block scales.
+int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
+                    const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
+                    bool exact, void* stream) {
+  LF_REQUIRE(m >= 1 && m <= 64, "decode path handles 1..64 tokens");
+  LF_REQUIRE(w->scales != nullptr, "decode takes fp32 block scales (prepare double-quant scales first)");
+  const GemvPlan pl = gemv_plan(m, w->n, w->k, device_cus(), lora ? lora->num_slices * lora->max_rank : 1);
+  LF_REQUIRE(w->n % pl.rows == 0, "output width must be a multiple of %d", pl.rows);
+  GemvParams p{};
+  p.x = x;
+  p.x_stride = x_stride;
+  p.m = int(m);
+  p.q = w->qweight;
+  p.scales = w->scales;
+  p.code = w->code;
+  p.n = int(w->n);
+  p.k = int(w->k);
+  p.bias = bias;
+  p.y = y;
+  p.y_stride = y_stride;
+  p.row_groups = pl.row_groups;
+  if (lora) {
+    const int64_t need = kWorkspaceHeader + int64_t(pl.units) * lora->num_slices * lora->max_rank * 4;
+    LF_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %lld bytes", (long long)need);
+    LF_REQUIRE(aligned16(workspace), "workspace must be 16-byte aligned");
+    LF_REQUIRE(kCounterOffset + 4 * int64_t(pl.units) <= kWorkspaceHeader, "too many shrink units");
+    p.a_store = lora->a_store;
+    p.a_offsets = lora->a_offsets;
+    p.b_store = lora->b_store;
+    p.b_offsets = lora->b_offsets;
+    p.b_strides = lora->b_strides;
+    p.ranks = lora->ranks;
+    p.lscales = lora->scales;
+    p.token_slots = lora->token_slots;
+    p.slice_offsets = lora->slice_offsets;
+    p.slices = lora->num_slices;
+    p.max_rank = lora->max_rank;
+    p.zw = lora->num_slices * lora->max_rank;
+    p.units = pl.units;
+    p.kz = pl.kz;
+    p.kz_len = pl.kz_len;
+    p.consumers = pl.row_groups;
+    p.producers = pl.producers;
+    char* ws = static_cast<char*>(workspace);
+    p.status = reinterpret_cast<int*>(ws + 8);
+    p.counters = reinterpret_cast<int*>(ws + kCounterOffset);
+    p.zp = reinterpret_cast<float*>(ws + kWorkspaceHeader);
+  }
+  const dim3 grid(unsigned(pl.grid));
+  auto s = static_cast<hipStream_t>(stream);
+  const bool lo = lora != nullptr;
+  if (m <= 2) launch_tile<1, 2>(exact, lo, grid, s, p);
+  else if (m <= 8) launch_tile<1, 8>(exact, lo, grid, s, p);
+  else if (m <= 16) launch_tile<1, 16>(exact, lo, grid, s, p);
+  else if (m <= 32) launch_tile<1, 32>(exact, lo, grid, s, p);
+  else launch_tile<2, 32>(exact, lo, grid, s, p);
+  LF_HIP(hipGetLastError());
+  return kOk;
+}
+
+}  // namespace lf

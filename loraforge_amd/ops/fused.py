@@ -112,21 +112,13 @@ def _workspace(device, stream: int, size: int):
 
 
 def _decode_takes_nested(m: int, n: int, k: int, dq_block: int) -> bool:
-    """Whether the decode kernel rebuilds double-quant scales itself.
+    """Whether the kernel for ``m`` tokens rebuilds double-quant scales itself.
 
-    It stages the second-level scales of a workgroup's rows in a 256-entry
-    window and copies the uint8 codes four at a time, so it needs K % 256 == 0
-    and a window that covers the group (mirrors the plan in
-    ``csrc/nf4_lora_decode.hip``); other decode shapes take prepared fp32 scales.
+    The prefill GEMM (m > 64) decodes the nested state per tile; the decode
+    kernel streams fp32 block scales, so decode calls take the prepared
+    scales, rebuilt once per weight and cached on the state.
     """
-    if m > 64:
-        return True
-    tm = (m + 15) // 16
-    waves = 4 if tm <= 2 or n % 128 else 8
-    nseg = 4 if tm <= 2 else 2
-    rows, krange = 16 * waves, 256 * nseg
-    span = ((rows - 1) * (k // 64) + krange // 64) // dq_block + 2
-    return k % 256 == 0 and span <= 256
+    return m > 64
 
 
 def _prepared_scales(state):
