@@ -94,6 +94,13 @@ __device__ __forceinline__ T sload(const T* base, int idx) {
 
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
+// Workgroup barrier after this wave's LDS accesses completed (lgkmcnt(0)),
+// without waiting for its global memory operations.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  barrier_only();
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -260,21 +267,24 @@ __device__ __forceinline__ void contract(const Frags<TL>& f, int kb, int kend, f
 
 
 // ---------------------------------------------------------------------------
-// LoRA wave (the last wave of every workgroup when LoRA is on).
+// LoRA (the last wave of every workgroup is the LoRA wave).
 //
 // Shrink: unit u = (token t = u / kz, k-slice u % kz) is computed at the
-// start of workgroup u % producers: zp[u][j] = sum over the slice of x[t][k] *
+// start of workgroup u % producers by all of its waves, while their first
+// weight copies are in flight: zp[u][j] = sum over the slice of x[t][k] *
 // A_g[j][k] for the slices * r rows of the token's adapter (MFMA, the token
 // row repeated across the 16 MFMA rows), stored with device-scope stores;
 // once they complete, counters[u] += consumers.
-// Expand: every workgroup waits until the units of its tile's tokens are
-// published, sums their k-slices (z = bf16(sum)), subtracts 1 from each
-// counter it read (so all counters are back to zero when the launch ends),
-// and computes bf16(scale_g * sum_j z[t][s r + j] * B_g[n][j]) for its
-// outputs on VALU, written in the layout of the base partial tiles.
-// Units are produced before any wait, by the first min(grid, CUs)
-// workgroups (one per CU), so every wait is for a workgroup that is already
-// running.
+// Expand: the LoRA wave of every workgroup waits, while the other waves
+// contract, until the units of its tile's tokens are published, sums their
+// k-slices into z = bf16(sum) in LDS and lists the tile's distinct slots;
+// last, it subtracts 1 from each counter it read, so all counters are back
+// to zero when the launch ends. Then every wave computes the expand of some
+// slots on MFMA, and the epilogue adds bf16(scale_g * sum_j z[t][s r + j] *
+// B_g[n][j]) to each routed token's output.
+// Units are produced before any wait, by workgroups below min(grid, CUs)
+// (one per CU, so all of them are running), and the plan keeps the units to
+// about half of those: every wait is for a workgroup that is already running.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int counter_load(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -351,51 +361,89 @@ __device__ void produce_units(const GemvParams& p, float* red, int wave, int lan
   }
 }
 
-// Token metadata of the tile, one entry per tile token (g = -1: base only).
+// Token metadata of the tile, one entry per tile token (g = -1: base only),
+// and the tile's distinct live slots (in order of first use).
 struct TileMeta {
   int g[32];
   int r[32];
   int stride[32];
   float scale[32];
   int64_t boff[32];
+  int dslot[32];
+  int dr[32];
+  int dstride[32];
+  int64_t dboff[32];
+  int nd;
+  int ready;  // set once the fields above are written (cleared at launch start)
 };
 
 // Up to 8 B values (16 bytes) of B row n of an adapter (offset boff, row
-// stride st, rank r) from rank j0; zeros past the rank.
-__device__ __forceinline__ uint4 load_b8(const GemvParams& p, int64_t boff, int st, int r, int n, int j0) {
-  const uint16_t* bp = p.b_store + boff + int64_t(n) * st + j0;
-  if (j0 >= r) return make_uint4(0, 0, 0, 0);
-  if ((st & 7) == 0) return *reinterpret_cast<const uint4*>(bp);  // stride >= 8: 16-byte rows
-  uint32_t h[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = j0 + e < r ? bp[e] : 0u;
-  return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+// stride st, rank r) from rank j0, zero past the rank or when !live. One
+// unconditional 16-byte load (branches here would serialize the callers'
+// loads): rows of stride >= 8 are 16-byte aligned (offsets are multiples of
+// 8 elements) and j0 + 8 <= stride whenever j0 < r; a row of stride 1, 2 or
+// 4 lies inside the aligned 16 bytes that hold its first element (inside
+// the adapter's N x stride region) and is shifted down by its position.
+struct B8 {
+  const uint16_t* src;  // aligned 16 bytes to load
+  int off;              // elements to shift down
+  int cnt;              // elements to keep
+};
+
+__device__ __forceinline__ B8 b8_at(const GemvParams& p, int64_t boff, int st, int r, int n, int j0, bool live) {
+  const int64_t e = boff + int64_t(n) * st + j0;
+  B8 b;
+  b.off = st >= 8 ? 0 : int(e & 7);
+  b.cnt = live ? min(8, r - j0) : 0;
+  // Nothing to keep (past the rank or dead): read the store's first 16
+  // bytes instead, which always exist.
+  b.src = p.b_store + (b.cnt > 0 ? e - b.off : 0);
+  return b;
 }
 
-__device__ __forceinline__ float dot8(const uint4& b, const uint4& z, float acc) {
-  const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
-  const uint32_t zw[4] = {z.x, z.y, z.z, z.w};
+__device__ __forceinline__ uint4 b8_fix(const uint4& v, const B8& b) {
+  const uint32_t w[5] = {v.x, v.y, v.z, v.w, 0u};
+  const int d = b.off >> 1;
+  uint32_t out[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    acc = __builtin_fmaf(bf16_lo(zw[q]), bf16_lo(bw[q]), acc);
-    acc = __builtin_fmaf(bf16_hi(zw[q]), bf16_hi(bw[q]), acc);
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t a = k + d < 4 ? w[k + d < 4 ? k + d : 4] : 0u;
+    const uint32_t c = k + d + 1 < 4 ? w[k + d + 1 < 4 ? k + d + 1 : 4] : 0u;
+    uint32_t o = (b.off & 1) ? ((a >> 16) | (c << 16)) : a;
+    if (2 * k >= b.cnt) o = 0u;
+    else if (2 * k + 1 >= b.cnt) o &= 0xffffu;
+    out[k] = o;
   }
-  return acc;
+  return make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-template <class TL>
-__device__ void lora_wave(const GemvParams& p, char* lds, int row0, int t0, int mt, int lane) {
-  constexpr int RT = TL::kRT;
-  constexpr int TT = TL::kTT;
-  constexpr int kTiles = RT * TT;
-  constexpr int kCols = TL::kR / 2;  // output columns per lane
-  float* dtile = reinterpret_cast<float*>(lds);
-  TileMeta* tm = reinterpret_cast<TileMeta*>(lds + kTiles * 1024);
-  // z, slice padded: [tile token][slice][64] bf16, zero past the rank.
-  uint16_t* zl = reinterpret_cast<uint16_t*>(lds + kTiles * 1024 + 1024);
-  float* stage = reinterpret_cast<float*>(lds + kTiles * 1024 + 1024 + TL::kXR * 192 * 2);
+__device__ __forceinline__ uint4 load_b8(const GemvParams& p, int64_t boff, int st, int r, int n, int j0,
+                                         bool live) {
+  const B8 b = b8_at(p, boff, st, r, n, j0, live);
+  return b8_fix(*reinterpret_cast<const uint4*>(b.src), b);
+}
 
-  // Tile token metadata.
+// LDS of the LoRA wave's ring region: its expand partial tiles, then the
+// tile metadata, z and the partial staging area.
+template <class TL>
+struct LoraLds {
+  static constexpr int kTiles = TL::kRT * TL::kTT;
+  static constexpr int kMeta = kTiles * 1024;
+  static constexpr int kZ = kMeta + 2048;                // z: [tile token][3 slices][64] bf16
+  static constexpr int kStage = kZ + TL::kXR * 192 * 2;  // 4 KiB of partials
+  static constexpr int kBytes = kStage + 4096;
+  static_assert(sizeof(TileMeta) <= 2048, "tile metadata");
+};
+
+// The LoRA wave: tile metadata and distinct slots, the wait for the tile's
+// units, z, and (last) the release of the units it read.
+template <class TL>
+__device__ void lora_prepare(const GemvParams& p, char* lds, int t0, int mt, int lane) {
+  using L = LoraLds<TL>;
+  TileMeta* tm = reinterpret_cast<TileMeta*>(lds + L::kMeta);
+  uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
+  float* stage = reinterpret_cast<float*>(lds + L::kStage);
+
   int g = -1, r = 0, stride = 1;
   float scale = 0.f;
   int64_t boff = 0;
@@ -420,28 +468,26 @@ __device__ void lora_wave(const GemvParams& p, char* lds, int row0, int t0, int 
     tm->scale[lane] = scale;
     tm->boff[lane] = boff;
   }
-  int bounds[4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) bounds[b] = b <= p.slices ? sload(p.slice_offsets, b) : 0;
-
-  // Expand operands, one token per lane (i = lane % 32) over half of the
-  // tile's columns (lane / 32): ranks 0..15 of the first 8 columns' B rows
-  // are requested before the wait for z.
-  const int i = lane & 31;
-  const int half = lane >> 5;
-  const bool live = i < mt && tm->g[i] >= 0;
-  const int ri = tm->r[i];
-  const int st = tm->stride[i];
-  const int64_t bo = tm->boff[i];
-  const float sc = tm->scale[i];
-  constexpr int kPre = kCols < 8 ? kCols : 8;
-  uint4 bv[kPre][2];
-#pragma unroll
-  for (int q = 0; q < kPre; ++q) {
-    const int n = row0 + half * kCols + q;
-    bv[q][0] = live ? load_b8(p, bo, st, ri, n, 0) : make_uint4(0, 0, 0, 0);
-    bv[q][1] = live ? load_b8(p, bo, st, ri, n, 8) : make_uint4(0, 0, 0, 0);
+  // Distinct live slots: one ballot per slot.
+  {
+    uint64_t left = __ballot(lane < 32 && g >= 0);
+    int nd = 0;
+    while (left) {
+      const int f = __builtin_ctzll(left);
+      const int gf = __builtin_amdgcn_readlane(g, f);
+      if (lane == f) {
+        tm->dslot[nd] = g;
+        tm->dr[nd] = r;
+        tm->dstride[nd] = stride;
+        tm->dboff[nd] = boff;
+      }
+      left &= ~__ballot(g == gf);
+      ++nd;
+    }
+    if (lane == 0) tm->nd = nd;
   }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the metadata is in LDS
+  if (lane == 0) *reinterpret_cast<volatile int*>(&tm->ready) = 1;
 
   // Wait until every unit of the tile's routed tokens is published.
   const int pairs = mt * p.kz;
@@ -464,12 +510,10 @@ __device__ void lora_wave(const GemvParams& p, char* lds, int row0, int t0, int 
   // The tile's partials are one contiguous block zp[t0 * kz .. (t0 + mt) * kz)
   // of zw values each (units of base-only tokens hold stale values and are
   // never used): up to 16 loads per lane at a time into LDS, then z[i][j] =
-  // bf16(sum over the kz <= 16 slices).
+  // bf16(sum over the kz <= 16 slices), slice padded and zero past the rank.
   for (int e = lane; e < TL::kXR * 192 / 8; e += 64) reinterpret_cast<uint4*>(zl)[e] = make_uint4(0, 0, 0, 0);
-  // Whole tokens per batch: per_token <= 1024 (the plan keeps
-  // tile tokens x zw x kz <= 1024 whenever kz > 1).
   const int per_token = p.kz * p.zw;
-  const int tpb = 1024 / per_token;
+  const int tpb = 1024 / per_token;  // whole tokens per batch (per_token <= 1024)
   const float* block = p.zp + int64_t(t0) * per_token;
   for (int i0 = 0; i0 < mt; i0 += tpb) {
     const int e0 = i0 * per_token;
@@ -478,71 +522,138 @@ __device__ void lora_wave(const GemvParams& p, char* lds, int row0, int t0, int 
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int e = q * 64 + lane;
-      v[q] = e < count ? shared_load(block + e0 + e) : 0.f;
+      v[q] = shared_load(block + e0 + min(e, count - 1));  // unconditional: no per-load branch
     }
 #pragma unroll
     for (int q = 0; q < 16; ++q) stage[q * 64 + lane] = v[q];
     for (int o = lane; o < count / p.kz; o += 64) {
-      const int il = o / p.zw;  // token within the batch
+      const int il = o / p.zw;
       const int j = o - il * p.zw;
       const float* src = stage + il * per_token + j;
       float z = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks)
-        if (ks < p.kz) z += src[ks * p.zw];
+      for (int ks = 0; ks < 16; ++ks) {
+        const float x = src[min(ks, p.kz - 1) * p.zw];
+        z += ks < p.kz ? x : 0.f;
+      }
       const int i = i0 + il;
       const int ri = tm->r[i];
       const int s = ri > 0 ? j / ri : 3;
       if (tm->g[i] >= 0 && s < p.slices) zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(z));
     }
   }
+  // Release the units read, after the partial loads (a later wait for a load
+  // would include these atomics; nothing waits for them).
   for (int c0 = 0; c0 < pairs; c0 += 64) {
     const int pr = c0 + lane;
-    const int i = pr / p.kz;
-    if (pr < pairs && tm->g[i] >= 0) counter_add(p.counters + t0 * p.kz + pr, -1);
+    const int it = pr / p.kz;
+    if (pr < pairs && tm->g[it] >= 0) counter_add(p.counters + t0 * p.kz + pr, -1);
   }
+}
 
-  // Expand: delta = bf16(scale * sum_j z[i][s*r + j] * B_g[n][j]), eight
-  // columns and 16 ranks of B at a time (the first batch is already here).
-  {
-    float acc[kCols];
+// Expand on MFMA, by the contraction waves (the LoRA wave finishes z last):
+// wave w takes the tile's distinct slots w, w + 7, ...; for each, delta[token][column] += z[token][s*64 + j] * B_g[column][j]
+// over ranks in steps of 32, with z rows of other slots' tokens masked to
+// zero, into tiles of the base layout (token rows x 16 columns). Columns of
+// other slices are masked on the B side. B fragments go four slots at a
+// time; the first batch is requested by expand_b_first as soon as a wave
+// has finished its contraction (the slot list is published before the wait
+// for z), so its latency overlaps that wait.
+constexpr int kExpandWaves = kWaves - 1;
+
+template <class TL>
+struct ExpandB {
+  uint4 bf[4][TL::kRT][2];
+};
+
+template <class TL>
+__device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMeta* tm, ExpandB<TL>& b, int d0,
+                                               int row0, int lane) {
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  const int nd = tm->nd;
 #pragma unroll
-    for (int q = 0; q < kCols; ++q) acc[q] = 0.f;
+  for (int q = 0; q < 4; ++q) {
+    const int d = d0 + q * kExpandWaves;
+    const bool live = d < nd;
+    const int dd = live ? d : 0;
 #pragma unroll
-    for (int c0 = 0; c0 < kCols; c0 += kPre) {
-      for (int j0 = 0; j0 < p.max_rank; j0 += 16) {
-        if (c0 > 0 || j0 > 0) {
+    for (int r = 0; r < TL::kRT; ++r)
 #pragma unroll
-          for (int q = 0; q < kPre; ++q) {
-            const int n = row0 + half * kCols + c0 + q;
-            bv[q][0] = live ? load_b8(p, bo, st, ri, n, j0) : make_uint4(0, 0, 0, 0);
-            bv[q][1] = live ? load_b8(p, bo, st, ri, n, j0 + 8) : make_uint4(0, 0, 0, 0);
+      for (int h = 0; h < 2; ++h)
+        b.bf[q][r][h] =
+            load_b8(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row0 + r * 16 + n, 32 * h + 8 * kg, live);
+  }
+}
+
+// Waits (LDS flag) for the LoRA wave's slot list, then requests this wave's
+// first batch of B fragments.
+template <class TL>
+__device__ __forceinline__ void expand_b_first(const GemvParams& p, const char* lds7, ExpandB<TL>& b, int row0,
+                                               int wave, int lane) {
+  const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds7 + LoraLds<TL>::kMeta);
+  while (*reinterpret_cast<const volatile int*>(&tm->ready) == 0) __builtin_amdgcn_s_sleep(1);
+  expand_b_batch<TL>(p, tm, b, wave, row0, lane);
+}
+
+template <class TL>
+__device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& b, const int (&bounds)[4], f32x4* out,
+                            int row0, int wave, int lane) {
+  using L = LoraLds<TL>;
+  constexpr int RT = TL::kRT;
+  constexpr int TT = TL::kTT;
+  const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds7 + L::kMeta);
+  const uint16_t* zl = reinterpret_cast<const uint16_t*>(lds7 + L::kZ);
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  f32x4 dacc[RT][TT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) dacc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int nd = tm->nd;
+  int cs[RT];  // slice of this lane's column in each row tile
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int col = row0 + r * 16 + n;
+    cs[r] = int(p.slices > 1 && col >= bounds[1]) + int(p.slices > 2 && col >= bounds[2]);
+  }
+  const int s_lo = int(p.slices > 1 && row0 >= bounds[1]) + int(p.slices > 2 && row0 >= bounds[2]);
+  const int s_hi = int(p.slices > 1 && row0 + TL::kR - 1 >= bounds[1]) + int(p.slices > 2 && row0 + TL::kR - 1 >= bounds[2]);
+  for (int d0 = wave; d0 < nd; d0 += 4 * kExpandWaves) {
+    if (d0 != wave) expand_b_batch<TL>(p, tm, b, d0, row0, lane);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int d = d0 + q * kExpandWaves;
+      if (d >= nd) break;  // uniform
+      const int g = tm->dslot[d];
+      const int rk = tm->dr[d];
+      for (int s = s_lo; s <= s_hi; ++s) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (32 * h >= rk) break;  // uniform
+          uint4 zf[TT];
+#pragma unroll
+          for (int t = 0; t < TT; ++t) {
+            const int tok = t * 16 + n;
+            const int tz = min(tok, TL::kXR - 1);
+            const uint4 v = *reinterpret_cast<const uint4*>(zl + (tz * 3 + s) * 64 + 32 * h + 8 * kg);
+            zf[t] = tm->g[tok] == g ? v : make_uint4(0, 0, 0, 0);
+          }
+#pragma unroll
+          for (int r = 0; r < RT; ++r) {
+            const uint4 bb = cs[r] == s ? b.bf[q][r][h] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) dacc[r][t] = mfma16(as_bf16x8(zf[t]), as_bf16x8(bb), dacc[r][t]);
           }
         }
-#pragma unroll
-        for (int q = 0; q < kPre; ++q) {
-          const int n = row0 + half * kCols + c0 + q;
-          int s = 0;
-          while (s + 1 < p.slices && n >= bounds[s + 1]) ++s;
-          const uint4* zr = reinterpret_cast<const uint4*>(zl + (i * 3 + s) * 64 + j0);
-          if (live && j0 < ri) {
-            acc[c0 + q] = dot8(bv[q][0], zr[0], acc[c0 + q]);
-            acc[c0 + q] = dot8(bv[q][1], zr[1], acc[c0 + q]);
-          }
-        }
-      }
-    }
-    // Into the base tile layout: tile (rt, tt), lane (col % 16) + 16 * (tok % 16 / 4), element tok % 4.
-    if (i < 16 * TT) {
-#pragma unroll
-      for (int q = 0; q < kCols; ++q) {
-        const int col = half * kCols + q;
-        const int c = (col / 16) * TT + i / 16;
-        const int l = (col & 15) + 16 * ((i & 15) >> 2);
-        dtile[(c * 64 + l) * 4 + (i & 3)] = live ? round_bf16(acc[q] * sc) : 0.f;
       }
     }
   }
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) out[(r * TT + t) * 64 + lane] = dacc[r][t];
 }
 
 // Copies of one stage (kSB blocks starting at block kb) into a ring slot.
@@ -588,10 +699,11 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   constexpr int TT = TL::kTT;
   constexpr int D = TL::kDepth;
   constexpr int kBase = kLora ? kWaves - 1 : kWaves;  // waves on the base contraction
-  // The LoRA wave keeps its delta tiles, tile metadata, z and a 4 KiB partial
-  // staging area in its own ring region plus 6 KiB.
-  static_assert(!kLora || RT * TT * 1024 + 1024 + XR * 192 * 2 + 4096 <= D * TL::kStage + 6144, "LoRA wave LDS");
-  __shared__ __attribute__((aligned(16))) char ring[kWaves * D * TL::kStage + (kLora ? 6144 : 0)];
+  // The LoRA wave keeps its expand tiles, tile metadata, z and a 4 KiB
+  // partial staging area in its own ring region (extended as needed).
+  constexpr int kLoraExtra = LoraLds<TL>::kBytes > D * TL::kStage ? LoraLds<TL>::kBytes - D * TL::kStage : 0;
+  static_assert(D * TL::kStage >= 2 * RT * TT * 1024, "base and expand tiles fit a ring region");
+  __shared__ __attribute__((aligned(16))) char ring[kWaves * D * TL::kStage + (kLora ? kLoraExtra : 0)];
   __shared__ float table[16];
   __shared__ __attribute__((aligned(16))) uint32_t pt[kExact ? 4 : 256 * kCopies];
   __shared__ float red[kLora ? kWaves * 192 : 1];
@@ -609,10 +721,16 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   const int nst = (kend - kb0 + TL::kSB - 1) / TL::kSB;
   char* myring = ring + wave * D * TL::kStage;
 
-  // Codebook through scalar loads (no vector load may wait behind the copies).
+  // Codebook (and the LoRA slice bounds) through scalar loads: no vector
+  // load may wait behind the copies.
   float cb[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) cb[i] = sload(p.code, i);
+  int bounds[4] = {0, 0, 0, 0};
+  if constexpr (kLora) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bounds[q] = q <= p.slices ? sload(p.slice_offsets, q) : 0;
+  }
 
 #pragma unroll
   for (int s = 0; s < D; ++s)
@@ -621,6 +739,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   if (threadIdx.x == 0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) table[i] = cb[i];
+    if constexpr (kLora)
+      reinterpret_cast<TileMeta*>(ring + kBase * D * TL::kStage + LoraLds<TL>::kMeta)->ready = 0;
   }
   if constexpr (!kExact) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -673,18 +793,32 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
 
   // Sum the waves' partial tiles: wave w writes its tiles into its own ring
   // (all of its copies have landed), then tile c = wave is summed by wave c.
-  // The LoRA wave writes the rounded, scaled expand deltas in the same layout.
+  // With LoRA the last wave prepares z meanwhile, then every contraction
+  // wave adds its share of the expand into a second tile set after its base
+  // tiles.
+  constexpr int kTiles = RT * TT;
+  char* lora7 = ring + kBase * D * TL::kStage;
+  ExpandB<TL> eb;
   if (kLora && wave == kBase) {
-    lora_wave<TL>(p, myring, row0, t0, mt, lane);
+    lora_prepare<TL>(p, myring, t0, mt, lane);
   } else {
     f32x4* red = reinterpret_cast<f32x4*>(myring);
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int t = 0; t < TT; ++t) red[(r * TT + t) * 64 + lane] = acc[r][t];
+    // After the ring stores: the compiler waits for every outstanding load
+    // before storing into the ring, which would include these.
+    if constexpr (kLora) expand_b_first<TL>(p, lora7, eb, row0, wave, lane);
   }
-  __syncthreads();
-  constexpr int kTiles = RT * TT;
+  auto delta_tiles = [&](int w) { return reinterpret_cast<f32x4*>(ring + w * D * TL::kStage + kTiles * 1024); };
+  // LDS-only barriers: a full fence here would also wait for the LoRA wave's
+  // counter releases and the early B loads.
+  if constexpr (kLora) {
+    lds_barrier();  // z and the tile metadata are in LDS
+    if (wave < kBase) expand_mfma<TL>(p, lora7, eb, bounds, delta_tiles(wave), row0, wave, lane);
+  }
+  lds_barrier();
   if (wave < kTiles) {
     const int r = wave / TT;
     const int t = wave % TT;
@@ -695,18 +829,28 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) sum[e] += v[e];
     }
-    f32x4 delta = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (kLora) delta = reinterpret_cast<const f32x4*>(ring + kBase * D * TL::kStage)[wave * 64 + lane];
+    f32x4 dsum = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kLora) {
+#pragma unroll
+      for (int w = 0; w < kBase; ++w) {
+        const f32x4 v = delta_tiles(w)[wave * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dsum[e] += v[e];
+      }
+    }
+    const TileMeta* tm = reinterpret_cast<const TileMeta*>(lora7 + LoraLds<TL>::kMeta);
     const int col = row0 + r * 16 + n;
     const float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int tok = t0 + t * 16 + 4 * g + e;
-      if (tok - t0 < mt) {
+      const int i = t * 16 + 4 * g + e;  // tile token
+      if (i < mt) {
         float v = round_bf16(sum[e]);
         if (p.bias) v = round_bf16(v + bias);
-        if constexpr (kLora) v += delta[e];  // zero for base-only tokens; the store rounds
-        p.y[int64_t(tok) * p.y_stride + col] = uint16_t(f32_to_bf16(v));
+        if constexpr (kLora) {
+          if (tm->g[i] >= 0) v += round_bf16(dsum[e] * tm->scale[i]);  // the store rounds
+        }
+        p.y[int64_t(t0 + i) * p.y_stride + col] = uint16_t(f32_to_bf16(v));
       }
     }
   }
