@@ -12,7 +12,7 @@ that cycles through 64 independent copies of the weight and the adapter set
 (> 1 GB in total, four times the 256 MB Infinity Cache), so every call
 streams from HBM; inputs are resident in HBM before timing starts.
 Also reported: the B = 1..64 sweep (us/call, GB/s, fraction of 8 TB/s), the
-c5 prefill (M=2048, K=4096, N=11008, NF4 + double quant, 8 segments of rank
+same linear without adapters at B = 1 and 64 (U = 0), the c5 prefill (M=2048, K=4096, N=11008, NF4 + double quant, 8 segments of rank
 32) in TFLOP/s against 2.5 PFLOP/s, and the reference's PyTorch CPU path on
 the host cores (cpu_baseline).
 """
@@ -157,14 +157,15 @@ def timed_replays(graph_full, reps: int, graph_tail, stream):
     return wall, start.elapsed_time(end) / 1e3
 
 
-def run_decode(work: DecodeWorkload, batch: int, steps: int, warmup: int, seed: int):
+def run_decode(work: DecodeWorkload, batch: int, steps: int, warmup: int, seed: int, lora: bool = True):
     import torch
 
     from loraforge_amd.ops import nf4_lora_linear
 
     x, slots, used = work.batch(batch, seed)
     out = torch.empty(batch, work.n, dtype=torch.bfloat16, device=work.device)
-    loras = [work.lora(layer, slots) for layer in range(work.layers)]
+    loras = [work.lora(layer, slots) if lora else None for layer in range(work.layers)]
+    used = used if lora else 0
 
     def call(layer):
         q, st = work.states[layer]
@@ -343,7 +344,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(head["frac"], 4),
             "traffic": measured_traffic(args.batch),
-            "kernel": "nf4_lora_decode_kernel",
+            "kernel": "nf4_gemv_kernel",
             "bytes_per_launch": head["bytes_per_call"],
             "us_per_launch": round(head["us_per_call"], 3),
             "timing": "HIP events on the graph-replay stream over the timed calls (includes the graph's "
@@ -357,6 +358,12 @@ def main() -> int:
             sweep[str(b)] = {key: round(r[key], 4) for key in ("us_per_call", "gbps", "frac")} | {"adapters_used": r["adapters_used"]}
             log(f"sweep B={b}: {r['us_per_call']:.2f} us/call, {r['gbps']:.0f} GB/s ({r['frac']:.1%})")
         result["sweep"] = sweep
+        base = {}
+        for b in (1, 64):
+            r = run_decode(work, b, 640, 64, seed=731 + b, lora=False)
+            base[str(b)] = {key: round(r[key], 4) for key in ("us_per_call", "gbps", "frac")}
+            log(f"base only B={b}: {r['us_per_call']:.2f} us/call, {r['gbps']:.0f} GB/s ({r['frac']:.1%})")
+        result["sweep_base_only"] = base
     del work
     torch.cuda.empty_cache()
     if not args.only and not args.no_prefill:

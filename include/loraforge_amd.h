@@ -96,7 +96,9 @@ int lf_row_expand(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets
  * ------------------------------------------------------------------------ */
 typedef struct lf_nf4_weight {
   const uint8_t* qweight; /* [N*K/2] */
-  const float* scales;    /* fp32 [N*K/64], or NULL when double-quantised */
+  const float* scales;    /* fp32 [N*K/64], or NULL when double-quantised
+                             (prefill only: decode, M <= 64, takes fp32
+                             scales, e.g. from lf_nf4_prepare_scales_dq) */
   const uint8_t* absmax_q;/* uint8 [N*K/64] (double quant) */
   const float* absmax2;   /* fp32 [ceil(N*K/64/dq_block)] */
   const float* code2;     /* fp32 [256] */
@@ -130,7 +132,8 @@ int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_
 
 /* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);
  * y [m, N] bf16 with row stride y_stride; bias bf16 [N] or NULL;
- * lora NULL for the base linear alone.
+ * lora NULL for the base linear alone. M <= 64 runs the decode kernel
+ * (fp32 block scales required), M > 64 the prefill GEMM.
  * flags: LF_EXACT_WEIGHTS makes the decode kernel multiply bf16_rne(code *
  * scale) weights (the reference's dequantised W, bit for bit); by default it
  * contracts bf16(code) and applies each fp32 block scale to the block's MFMA

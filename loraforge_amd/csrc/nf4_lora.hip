@@ -1,15 +1,9 @@
 // C-ABI entry of the fused NF4 + multi-LoRA linear: argument validation and
 // dispatch between the decode kernel (M <= 64 tokens) and the prefill GEMM.
-#include <algorithm>
-
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
 
 namespace lf {
-int64_t decode_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
-int launch_nf4_lora_decode(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
-                           const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                           void* workspace, int64_t workspace_bytes, bool exact, void* stream);
 int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
@@ -24,9 +18,7 @@ constexpr int64_t kDecodeMaxTokens = 64;
 extern "C" int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices,
                                               int32_t max_rank) {
   if (m < 0 || n <= 0 || k <= 0 || num_slices < 1 || max_rank < 1) return -1;
-  if (m <= lf::kDecodeMaxTokens)
-    return std::max(lf::decode_workspace_bytes(m, n, k, num_slices, max_rank),
-                    lf::gemv_workspace_bytes(m, n, k, num_slices, max_rank));
+  if (m <= lf::kDecodeMaxTokens) return lf::gemv_workspace_bytes(m, n, k, num_slices, max_rank);
   return lf::prefill_workspace_bytes(m, n, k, num_slices, max_rank);
 }
 
@@ -54,12 +46,15 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
                "incomplete LoRA descriptor");
     LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
   }
-  if (m <= lf::kDecodeMaxTokens && w->scales)
+  if (m <= lf::kDecodeMaxTokens) {
+    // The decode kernel streams fp32 block scales (as the reference serves
+    // decode from prepare_scales output): nested states go through
+    // lf_nf4_prepare_scales_dq once per weight.
+    LF_REQUIRE(w->scales != nullptr,
+               "decode (M <= 64) takes fp32 block scales: build them with lf_nf4_prepare_scales_dq");
     return lf::launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
                                (flags & LF_EXACT_WEIGHTS) != 0, stream);
-  if (m <= lf::kDecodeMaxTokens)
-    return lf::launch_nf4_lora_decode(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
-                                      (flags & LF_EXACT_WEIGHTS) != 0, stream);
+  }
   return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, stream);
 }
 
