@@ -124,10 +124,11 @@ typedef struct lf_lora {
 } lf_lora;
 
 /* Bytes of device workspace lf_nf4_lora_linear needs for this problem. The
- * first 64 KiB hold control counters that must be zero before the first
- * call; every completed call leaves them zero again (decode and prefill
- * calls may share one workspace). Calls that share one workspace must not
- * overlap in time. */
+ * first 128 KiB are the decode kernel's control header (a launch word, a
+ * status word and the shrink partials, each tagged with the call that wrote
+ * it); it must be zero before the first call and is never reset between
+ * calls. Decode and prefill calls may share one workspace; calls that share
+ * one workspace must not overlap in time. */
 int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices, int32_t max_rank);
 
 /* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);

@@ -12,11 +12,12 @@ namespace lf {
 
 constexpr int kNf4Block = 64;
 
-// Every fused-linear workspace starts with this control header: the decode
-// kernel's counters (zero between calls; each completed call leaves them
-// zero). No other kernel writes it, so decode and prefill calls can share
-// one workspace.
-constexpr int64_t kWorkspaceHeader = 65536;
+// Every fused-linear workspace starts with this control header, owned by the
+// decode kernel: its launch word, status word and tagged shrink partials
+// (entries are valid only for the call whose tag they carry, so nothing is
+// reset between calls). No other kernel writes it, so decode and prefill
+// calls can share one workspace.
+constexpr int64_t kWorkspaceHeader = 131072;
 
 // Codebook lookup by a byte offset (nibble * 4) into a 16-entry fp32 table in
 // LDS. All lanes read at most 16 distinct words, so the read is bank-conflict

@@ -77,11 +77,12 @@ struct GemvParams {
   int units;      // shrink units: m * kz (unit u = token u / kz, k-slice u % kz)
   int kz;         // k-slices per token
   int kz_len;     // k per slice (multiple of 64)
-  int consumers;  // workgroups that read each unit: row_groups
   int producers;  // workgroups b < producers make units b, b + producers, ...
   int* status;    // set to 1 when a bounded wait times out
-  int* counters;  // [units] published-unit counters, zero between calls
-  float* zp;      // [units][zw] shrink partial sums
+  uint32_t* epoch;   // the call's tag is epoch + 1
+  uint32_t* groups;  // [8] arrival counts, 128 bytes apart (workgroup b counts in b % 8)
+  uint32_t* total;   // groups complete in this call
+  uint64_t* zp;      // [units][zw] shrink partial sums as (tag << 32) | fp32 bits
 };
 
 constexpr int kSpinLimit = 1 << 20;
@@ -269,94 +270,258 @@ __device__ __forceinline__ void contract(const Frags<TL>& f, int kb, int kend, f
 // ---------------------------------------------------------------------------
 // LoRA (the last wave of every workgroup is the LoRA wave).
 //
-// Shrink: unit u = (token t = u / kz, k-slice u % kz) is computed at the
-// start of workgroup u % producers by all of its waves, while their first
-// weight copies are in flight: zp[u][j] = sum over the slice of x[t][k] *
-// A_g[j][k] for the slices * r rows of the token's adapter (MFMA, the token
-// row repeated across the 16 MFMA rows), stored with device-scope stores;
-// once they complete, counters[u] += consumers.
-// Expand: the LoRA wave of every workgroup waits, while the other waves
-// contract, until the units of its tile's tokens are published, sums their
-// k-slices into z = bf16(sum) in LDS and lists the tile's distinct slots;
-// last, it subtracts 1 from each counter it read, so all counters are back
-// to zero when the launch ends. Then every wave computes the expand of some
-// slots on MFMA, and the epilogue adds bf16(scale_g * sum_j z[t][s r + j] *
-// B_g[n][j]) to each routed token's output.
+// Shrink: unit u = (token t = u / kz, k-slice u % kz) is computed early in
+// workgroup u % producers: all eight waves contract x[t] with the slices * r
+// rows of the token's adapter A_g over the slice (MFMA, the token row
+// repeated across the 16 MFMA rows); the LoRA wave sums their partial rows
+// and stores zp[u][j] with device-scope 64-bit stores, each value paired
+// with the call's tag. The fragments of a workgroup's first unit are
+// requested between its first and second weight stages, so they are not
+// queued behind the whole prologue.
+// Call tag: every workgroup reads the epoch word at its start; the call's
+// tag is epoch + 1. When its work is done, the LoRA wave counts the
+// workgroup in (one counter per blockIdx % 8, so no single address takes
+// every atomic); the last of a group counts the group in, and the last group
+// resets the counters and moves the epoch on. Every workgroup has read the
+// epoch before it counts in, so all workgroups of a call see the same tag
+// and no earlier call used it (tags cycle through 1 .. 2^32 - 1; zero never
+// marks data, so a zeroed workspace holds no valid entry). An entry is valid
+// for a call iff its tag is the call's: nothing is reset between calls.
+// Expand: the LoRA wave of every workgroup lists its tile's tokens and
+// distinct slots, then polls the partials of its routed tokens until all
+// carry the call's tag and sums their k-slices into z = bf16(sum) in LDS.
+// Meanwhile the other waves contract the base; then they compute the expand
+// of the tile's slots on MFMA, and the epilogue adds
+// bf16(scale_g * sum_j z[t][s r + j] * B_g[n][j]) to each routed token.
 // Units are produced before any wait, by workgroups below min(grid, CUs)
 // (one per CU, so all of them are running), and the plan keeps the units to
 // about half of those: every wait is for a workgroup that is already running.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int counter_load(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+constexpr int kProd = kWaves - 1;  // contraction waves: they compute the shrink partials
+constexpr int kBatch = 10;         // MFMA steps per wave and batch (kProd * kBatch >= 64 steps)
+
+__device__ __forceinline__ void tagged_store(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void counter_add(int* p, int v) {
-  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void shared_store(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float shared_load(const float* p) {
+__device__ __forceinline__ uint64_t tagged_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// All waves of a producing workgroup share its units at the start, while
-// their first weight copies are in flight: wave w takes the 32-k MFMA steps
-// w, w + 8, ... of the unit's slice, the partial rows meet in red[wave][j],
-// and the LoRA wave (publisher) sums, stores and publishes them. Every
-// branch here is uniform over the workgroup (barriers inside).
-__device__ void produce_units(const GemvParams& p, float* red, int wave, int lane, bool publisher) {
+// A per-lane zero the compiler cannot see through: an atomic on a provably
+// uniform address is turned into a wave-wide one whose result is waited for
+// on the spot.
+__device__ __forceinline__ uint32_t opaque_zero() {
+  uint32_t z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
+// Counts this workgroup in (lane 0); the old count is returned in lane 0 and
+// nothing waits for it until depart_finish.
+__device__ __forceinline__ uint32_t depart_issue(const GemvParams& p, int lane) {
+  uint32_t* counter = p.groups + 32 * (blockIdx.x & 7) + opaque_zero();
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return old;
+}
+
+// The last workgroup of its group counts the group in; the last group
+// resets the counts and moves the epoch on.
+__device__ __forceinline__ void depart_finish(const GemvParams& p, uint32_t old, uint32_t epoch, int lane) {
+  if (lane != 0) return;
+  const uint32_t g = blockIdx.x & 7;
+  const uint32_t members = (gridDim.x - g + 7) / 8;
+  if (old != members - 1) return;
+  __hip_atomic_store(p.groups + 32 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t groups = gridDim.x < 8 ? gridDim.x : 8u;
+  if (__hip_atomic_fetch_add(p.total, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != groups - 1) return;
+  __hip_atomic_store(p.total, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(p.epoch, epoch + 1 == 0xffffffffu ? 0u : epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct Unit {
+  int t;      // token
+  int ks;     // k-slice
+  int rows;   // slices * rank
+  int kb;     // first k of the slice
+  int steps;  // 32-k MFMA steps in the slice
+  int64_t aoff;
+};
+
+// Unit u's token, adapter rows and k-slice (scalar loads); false when the
+// token has no adapter (base only), so nothing is produced.
+__device__ __forceinline__ bool unit_of(const GemvParams& p, int u, Unit& un) {
+  un.t = u / p.kz;
+  un.ks = u - un.t * p.kz;
+  const int ks = un.ks;
+  const int g = sload(p.token_slots, un.t);
+  if (g < 0) return false;
+  const int r = sload(p.ranks, g);
+  if (r <= 0 || r > p.max_rank) return false;
+  un.aoff = sload(p.a_offsets, g);
+  un.rows = p.slices * r;
+  un.kb = ks * p.kz_len;
+  un.steps = (min(p.k, un.kb + p.kz_len) - un.kb) >> 5;
+  if (un.steps <= 0) {  // an empty trailing slice: zero partials, read at k = 0
+    un.kb = 0;
+    un.steps = 0;
+  }
+  return true;
+}
+
+// Partial of value j of unit (token t, k-slice ks): entry (t * zw + j) * kz +
+// ks, so the kz partials a consumer sums for one value are adjacent.
+__device__ __forceinline__ int64_t partial_index(const GemvParams& p, const Unit& un, int j) {
+  return (int64_t(un.t) * p.zw + j) * p.kz + un.ks;
+}
+
+// x and A fragments of the MFMA steps st0 + i * stride (i < kBatch) of rows
+// j0 .. j0 + 15 of a unit. Loads are unconditional (steps past the slice
+// read its last step and contribute zero x) so that they are not serialised
+// by branches.
+template <int NB>
+struct UnitFragsN {
+  u32x4 xv[NB];
+  u32x4 av[NB];
+};
+using UnitFrags = UnitFragsN<kBatch>;
+
+// A 16-byte global load the compiler does not track. While direct LDS copies
+// are in flight, the compiler waits for every outstanding memory operation
+// before using any tracked load result; these fragments are requested
+// between the first and second weight stages and are known to have landed
+// once the second stage has (loads complete in order).
+__device__ __forceinline__ u32x4 global_load128_untracked(const void* ptr) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr) : "memory");
+  return v;
+}
+
+// The same for the lanes of `lanes` only (the others keep zero and issue no
+// memory request): the whole exec change stays inside the statement.
+__device__ __forceinline__ u32x4 global_load128_untracked_masked(const void* ptr, uint64_t lanes) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  uint64_t saved;
+  asm volatile(
+      "s_and_saveexec_b64 %1, %3\n\t"
+      "global_load_dwordx4 %0, %2, off\n\t"
+      "s_mov_b64 exec, %1"
+      : "+v"(v), "=&s"(saved)
+      : "v"(ptr), "s"(lanes)
+      : "memory", "exec");
+  return v;
+}
+
+template <bool kUntracked, int NB>
+__device__ __forceinline__ void unit_frags(const GemvParams& p, const Unit& un, int j0, int st0, int stride, int lane,
+                                           UnitFragsN<NB>& f) {
+  const int jn = lane & 15;
+  const int kg = lane >> 4;
+  const uint16_t* xrow = p.x + int64_t(un.t) * p.x_stride + un.kb + 8 * kg;
+  const int j = j0 + jn;
+  const uint16_t* arow = p.a_store + un.aoff + int64_t(j < un.rows ? j : un.rows - 1) * p.k + un.kb + 8 * kg;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int st = st0 + i * stride;
+    const int sc = st < un.steps ? st : max(un.steps - 1, 0);
+    if constexpr (kUntracked) {
+      // Only MFMA row 0 needs the token's x (the other rows stay zero and
+      // their results are ignored): 64 bytes per step instead of 1 KiB.
+      f.xv[i] = global_load128_untracked_masked(xrow + 32 * sc, 0x0001000100010001ull);
+      f.av[i] = global_load128_untracked(arow + 32 * sc);
+    } else {
+      f.xv[i] = *reinterpret_cast<const u32x4*>(xrow + 32 * sc);
+      f.av[i] = *reinterpret_cast<const u32x4*>(arow + 32 * sc);
+    }
+  }
+}
+
+// Ties every fragment register to a wait already made (no use may be
+// scheduled above it).
+__device__ __forceinline__ void tie_frags(UnitFrags& f) {
+#pragma unroll
+  for (int i = 0; i < kBatch; ++i) {
+    tie(f.xv[i]);
+    tie(f.av[i]);
+  }
+}
+
+template <int NB>
+__device__ __forceinline__ f32x4 unit_mfma(const UnitFragsN<NB>& f, const Unit& un, int st0, int stride, f32x4 c) {
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    c = mfma16(vec_bf16x8(st0 + i * stride < un.steps ? f.xv[i] : zero), vec_bf16x8(f.av[i]), c);
+  return c;
+}
+
+// Contraction wave w (< kProd) sums the MFMA steps w, w + kProd, ... of
+// every 16-row group of the workgroup's first unit into red[w][j] (j < rows;
+// higher j are never read). pre holds the first batch of row group 0 (already
+// landed); anything beyond it is loaded here. Then the wave counts itself
+// in (LDS) so the LoRA wave can publish without a workgroup barrier.
+__device__ void first_unit_partials(const GemvParams& p, const Unit& un, UnitFrags& pre, float* red, int* done,
+                                    int wave, int lane) {
+  tie_frags(pre);
+  const int jn = lane & 15;
+  const int kg = lane >> 4;
+  for (int j0 = 0; j0 < un.rows; j0 += 16) {
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+    int st0 = wave;
+    if (j0 == 0) {
+      c = unit_mfma(pre, un, st0, kProd, c);
+      st0 += kBatch * kProd;
+    }
+    // Anything beyond the first batch (ranks above 16, long slices) in small
+    // batches: this runs inside the base loop, where registers are scarce.
+    for (; st0 < un.steps; st0 += 2 * kProd) {
+      UnitFragsN<2> f;
+      unit_frags<false>(p, un, j0, st0, kProd, lane, f);
+      c = unit_mfma(f, un, st0, kProd, c);
+    }
+    // Row 0 of C (lanes 0..15, element 0) holds this wave's partial of z[j].
+    if (kg == 0) red[wave * 192 + j0 + jn] = c[0];
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the partial rows are in LDS
+  if (lane == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The LoRA wave: waits (LDS) until the contraction waves have written the
+// first unit's partial rows, sums and stores them with the call's tag.
+__device__ void publish_first_unit(const GemvParams& p, const float* red, const int* done, const Unit& un,
+                                   uint32_t tag, int lane) {
+  const int rows = un.rows;
+  while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kProd)
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const int jj = q * 64 + lane;
+    if (jj < rows) {
+      float v = 0.f;
+      for (int w = 0; w < kProd; ++w) v += red[w * 192 + jj];
+      tagged_store(p.zp + partial_index(p, un, jj), v, tag);
+    }
+  }
+}
+
+// The LoRA wave alone: the workgroup's other units (only when there are
+// more units than producers, i.e. small grids), each contracted whole by
+// this wave and stored with the call's tag.
+__device__ void produce_other_units(const GemvParams& p, uint32_t tag, int lane) {
   if (blockIdx.x >= unsigned(p.producers)) return;
-  for (int u = blockIdx.x; u < p.units; u += p.producers) {
-    const int t = u / p.kz;
-    const int ks = u - t * p.kz;
-    const int g = sload(p.token_slots, t);
-    if (g < 0) continue;
-    const int r = sload(p.ranks, g);
-    if (r <= 0 || r > p.max_rank) continue;  // base only
-    const int64_t aoff = sload(p.a_offsets, g);
-    const int rows = p.slices * r;
-    const int kb = ks * p.kz_len;
-    const int steps = (min(p.k, kb + p.kz_len) - kb) >> 5;
-    const int jn = lane & 15;
-    const int kg = lane >> 4;
-    const uint16_t* xrow = p.x + int64_t(t) * p.x_stride + kb + 8 * kg;
-    for (int j0 = 0; j0 < rows; j0 += 16) {
-      const int j = j0 + jn;
-      const uint16_t* arow = p.a_store + aoff + int64_t(j < rows ? j : rows - 1) * p.k + kb + 8 * kg;
+  const int jn = lane & 15;
+  const int kg = lane >> 4;
+  for (int u = blockIdx.x + p.producers; u < p.units; u += p.producers) {
+    Unit un;
+    if (!unit_of(p, u, un)) continue;
+    for (int j0 = 0; j0 < un.rows; j0 += 16) {
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
-      for (int st0 = wave; st0 < steps; st0 += 8 * kWaves) {
-        uint4 xv[8], av[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int st = st0 + i * kWaves;
-          const bool ok = st < steps;
-          xv[i] = ok ? *reinterpret_cast<const uint4*>(xrow + 32 * st) : make_uint4(0, 0, 0, 0);
-          av[i] = ok ? *reinterpret_cast<const uint4*>(arow + 32 * st) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) c = mfma16(as_bf16x8(xv[i]), as_bf16x8(av[i]), c);
+      for (int st0 = 0; st0 < un.steps; st0 += kBatch) {
+        UnitFrags f;
+        unit_frags<false, kBatch>(p, un, j0, st0, 1, lane, f);
+        c = unit_mfma(f, un, st0, 1, c);
       }
-      // Row 0 of C (lanes 0..15, element 0) holds this wave's partial of z[j0 + lane].
-      if (kg == 0) red[wave * 192 + j0 + jn] = c[0];
-    }
-    __syncthreads();
-    float v[3];
-    if (publisher) {
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        const int jj = q * 64 + lane;
-        v[q] = 0.f;
-        if (jj < rows)
-          for (int w = 0; w < kWaves; ++w) v[q] += red[w * 192 + jj];
-      }
-    }
-    __syncthreads();  // red is free again
-    if (publisher) {
-#pragma unroll
-      for (int q = 0; q < 3; ++q)
-        if (q * 64 + lane < rows) shared_store(p.zp + int64_t(u) * p.zw + q * 64 + lane, v[q]);
-      wait_vm<0>();  // partial stores complete
-      if (lane == 0) counter_add(p.counters + u, p.consumers);
+      if (kg == 0 && j0 + jn < un.rows) tagged_store(p.zp + partial_index(p, un, j0 + jn), c[0], tag);
     }
   }
 }
@@ -417,50 +582,59 @@ __device__ __forceinline__ uint4 b8_fix(const uint4& v, const B8& b) {
   return make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-__device__ __forceinline__ uint4 load_b8(const GemvParams& p, int64_t boff, int st, int r, int n, int j0,
-                                         bool live) {
-  const B8 b = b8_at(p, boff, st, r, n, j0, live);
-  return b8_fix(*reinterpret_cast<const uint4*>(b.src), b);
-}
-
-// LDS of the LoRA wave's ring region: its expand partial tiles, then the
-// tile metadata, z and the partial staging area.
+// LDS of the LoRA stages, an array that never receives direct copies (so
+// stores into it do not wait for copies in flight): the tile metadata, z and
+// the partial staging area.
 template <class TL>
 struct LoraLds {
-  static constexpr int kTiles = TL::kRT * TL::kTT;
-  static constexpr int kMeta = kTiles * 1024;
-  static constexpr int kZ = kMeta + 2048;                // z: [tile token][3 slices][64] bf16
+  static constexpr int kMeta = 0;
+  static constexpr int kZ = 2048;                        // z: [tile token][3 slices][64] bf16
   static constexpr int kStage = kZ + TL::kXR * 192 * 2;  // 4 KiB of partials
   static constexpr int kBytes = kStage + 4096;
   static_assert(sizeof(TileMeta) <= 2048, "tile metadata");
 };
 
-// The LoRA wave: tile metadata and distinct slots, the wait for the tile's
-// units, z, and (last) the release of the units it read.
-template <class TL>
-__device__ void lora_prepare(const GemvParams& p, char* lds, int t0, int mt, int lane) {
-  using L = LoraLds<TL>;
-  TileMeta* tm = reinterpret_cast<TileMeta*>(lds + L::kMeta);
-  uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
-  float* stage = reinterpret_cast<float*>(lds + L::kStage);
+// The LoRA wave, part 1a (before the workgroup's table barrier, while
+// nothing else is outstanding in this wave): the slot of tile token `lane`
+// and its adapter's metadata, two round trips. Base-only tokens and lanes
+// past the tile read the slice bounds instead (at least 8 valid bytes; the
+// values are discarded), since the table may hold no slot at all.
+struct TokenMeta {
+  int g;
+  int r;
+  int stride;
+  float scale;
+  int64_t boff;
+};
 
-  int g = -1, r = 0, stride = 1;
-  float scale = 0.f;
-  int64_t boff = 0;
-  if (lane < mt) {
-    g = p.token_slots[t0 + lane];
-    if (g >= 0) {
-      r = p.ranks[g];
-      if (r <= 0 || r > p.max_rank) {
-        g = -1;
-        r = 0;
-      } else {
-        stride = p.b_strides[g];
-        scale = p.lscales[g];
-        boff = p.b_offsets[g];
-      }
-    }
+__device__ __forceinline__ TokenMeta token_meta(const GemvParams& p, int t0, int mt, int lane) {
+  TokenMeta m;
+  m.g = p.token_slots[t0 + min(lane, mt - 1)];
+  if (lane >= mt) m.g = -1;
+  const bool live = m.g >= 0;
+  const void* fb = p.slice_offsets;
+  m.r = *(live ? p.ranks + m.g : static_cast<const int32_t*>(fb));
+  m.stride = *(live ? p.b_strides + m.g : static_cast<const int32_t*>(fb));
+  m.scale = *(live ? p.lscales + m.g : static_cast<const float*>(fb));
+  m.boff = *(live ? p.b_offsets + m.g : static_cast<const int64_t*>(fb));
+  if (!live || m.r <= 0 || m.r > p.max_rank) {
+    m.g = -1;
+    m.r = 0;
+    m.stride = 1;
+    m.scale = 0.f;
+    m.boff = 0;
   }
+  return m;
+}
+
+// The LoRA wave, part 1b (after the table barrier): tile metadata and
+// distinct slots into LDS, then the ready flag.
+template <class TL>
+__device__ void lora_meta(char* lds, const TokenMeta& m, int lane) {
+  TileMeta* tm = reinterpret_cast<TileMeta*>(lds + LoraLds<TL>::kMeta);
+  const int g = m.g, r = m.r, stride = m.stride;
+  const float scale = m.scale;
+  const int64_t boff = m.boff;
   if (lane < 32) {
     tm->g[lane] = g;
     tm->r[lane] = r;
@@ -469,85 +643,101 @@ __device__ void lora_prepare(const GemvParams& p, char* lds, int t0, int mt, int
     tm->boff[lane] = boff;
   }
   // Distinct live slots: one ballot per slot.
-  {
-    uint64_t left = __ballot(lane < 32 && g >= 0);
-    int nd = 0;
-    while (left) {
-      const int f = __builtin_ctzll(left);
-      const int gf = __builtin_amdgcn_readlane(g, f);
-      if (lane == f) {
-        tm->dslot[nd] = g;
-        tm->dr[nd] = r;
-        tm->dstride[nd] = stride;
-        tm->dboff[nd] = boff;
-      }
-      left &= ~__ballot(g == gf);
-      ++nd;
+  uint64_t left = __ballot(lane < 32 && g >= 0);
+  int nd = 0;
+  while (left) {
+    const int f = __builtin_ctzll(left);
+    const int gf = __builtin_amdgcn_readlane(g, f);
+    if (lane == f) {
+      tm->dslot[nd] = g;
+      tm->dr[nd] = r;
+      tm->dstride[nd] = stride;
+      tm->dboff[nd] = boff;
     }
-    if (lane == 0) tm->nd = nd;
+    left &= ~__ballot(g == gf);
+    ++nd;
   }
+  if (lane == 0) tm->nd = nd;
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the metadata is in LDS
-  if (lane == 0) *reinterpret_cast<volatile int*>(&tm->ready) = 1;
+  if (lane == 0) *(volatile __attribute__((address_space(3))) int*)(&tm->ready) = 1;
+}
 
-  // Wait until every unit of the tile's routed tokens is published.
-  const int pairs = mt * p.kz;
-  for (int spins = 0;; ++spins) {
-    bool ready = true;
-    for (int c0 = 0; c0 < pairs; c0 += 64) {
-      const int pr = c0 + lane;
-      const int i = pr / p.kz;
-      const bool need = pr < pairs && tm->g[i] >= 0;
-      const int v = need ? counter_load(p.counters + t0 * p.kz + pr) : 1;
-      ready = ready && __all(v > 0);
-    }
-    if (ready) break;
-    if (spins > kSpinLimit) {
-      if (lane == 0) __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-    __builtin_amdgcn_s_sleep(2);
-  }
-  // The tile's partials are one contiguous block zp[t0 * kz .. (t0 + mt) * kz)
-  // of zw values each (units of base-only tokens hold stale values and are
-  // never used): up to 16 loads per lane at a time into LDS, then z[i][j] =
-  // bf16(sum over the kz <= 16 slices), slice padded and zero past the rank.
+// a / d for 0 <= a, d <= 1024 through a multiply: inverse = ceil(2^21 / d);
+// the rounding error stays below 1024 / 2^21 < 1 / 1024 <= 1 - frac(a / d).
+__device__ __forceinline__ uint32_t small_inverse(int d) { return ((1u << 21) + uint32_t(d) - 1) / uint32_t(d); }
+__device__ __forceinline__ int small_div(int a, uint32_t inverse) { return int((uint32_t(a) * inverse) >> 21); }
+
+// The LoRA wave, part 2: z of the tile. The tile's partials are one
+// contiguous block: token i's value j has its KZ k-slice partials at
+// ((t0 + i) * zw + j) * KZ .. + KZ. Each lane owns up to 16 / KZ values of a
+// batch of whole tokens; the entries a routed token needs (j < slices * r)
+// are polled until all carry the call's tag, then each value is summed in
+// registers, z[i][j] = bf16(sum), and stored slice padded into LDS (zero past
+// the rank). Entries of base-only tokens and past the rank are never waited
+// for or used. KZ (k-slices per token) is a power of two up to 16.
+template <class TL, int KZ>
+__device__ void lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, uint32_t tag, int lane) {
+  using L = LoraLds<TL>;
+  constexpr int kOut = 16 / KZ;  // values per lane and batch
+  const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + L::kMeta);
+  uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
   for (int e = lane; e < TL::kXR * 192 / 8; e += 64) reinterpret_cast<uint4*>(zl)[e] = make_uint4(0, 0, 0, 0);
-  const int per_token = p.kz * p.zw;
-  const int tpb = 1024 / per_token;  // whole tokens per batch (per_token <= 1024)
-  const float* block = p.zp + int64_t(t0) * per_token;
+  const int tpb = max(1, (64 * kOut) / p.zw);  // whole tokens per batch (zw <= 192)
+  const uint32_t inv_zw = small_inverse(p.zw);
   for (int i0 = 0; i0 < mt; i0 += tpb) {
-    const int e0 = i0 * per_token;
-    const int count = min(tpb, mt - i0) * per_token;
-    float v[16];
+    const int nout = min(tpb, mt - i0) * p.zw;  // values in this batch
+    const uint64_t* block = p.zp + (int64_t(t0 + i0) * p.zw) * KZ;
+    int il[kOut], jv[kOut];
+    bool need[kOut];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int e = q * 64 + lane;
-      v[q] = shared_load(block + e0 + min(e, count - 1));  // unconditional: no per-load branch
+    for (int q = 0; q < kOut; ++q) {
+      const int o = min(q * 64 + lane, nout - 1);
+      il[q] = small_div(o, inv_zw);
+      jv[q] = o - il[q] * p.zw;
+      const int i = i0 + il[q];
+      need[q] = q * 64 + lane < nout && tm->g[i] >= 0 && jv[q] < p.slices * tm->r[i];
+    }
+    uint64_t v[kOut][KZ];
+    for (int spins = 0;; ++spins) {
+#pragma unroll
+      for (int q = 0; q < kOut; ++q)
+#pragma unroll
+        for (int ks = 0; ks < KZ; ++ks)  // unconditional: no per-load branch
+          v[q][ks] = tagged_load(block + int64_t(min(q * 64 + lane, nout - 1)) * KZ + ks);
+      bool ok = true;
+#pragma unroll
+      for (int q = 0; q < kOut; ++q)
+#pragma unroll
+        for (int ks = 0; ks < KZ; ++ks) ok = ok && (!need[q] || uint32_t(v[q][ks] >> 32) == tag);
+      if (__all(ok)) break;
+      if (spins > kSpinLimit) {
+        if (lane == 0) __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
-    for (int q = 0; q < 16; ++q) stage[q * 64 + lane] = v[q];
-    for (int o = lane; o < count / p.kz; o += 64) {
-      const int il = o / p.zw;
-      const int j = o - il * p.zw;
-      const float* src = stage + il * per_token + j;
+    for (int q = 0; q < kOut; ++q) {
       float z = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < 16; ++ks) {
-        const float x = src[min(ks, p.kz - 1) * p.zw];
-        z += ks < p.kz ? x : 0.f;
-      }
-      const int i = i0 + il;
+      for (int ks = 0; ks < KZ; ++ks) z += __uint_as_float(uint32_t(v[q][ks]));
+      const int i = i0 + il[q];
+      const int j = jv[q];
       const int ri = tm->r[i];
-      const int s = ri > 0 ? j / ri : 3;
-      if (tm->g[i] >= 0 && s < p.slices) zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(z));
+      const int s = int(j >= ri) + int(j >= 2 * ri) + int(j >= 3 * ri);  // slice of value j (3: past them)
+      if (need[q] && s < p.slices) zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(z));
     }
   }
-  // Release the units read, after the partial loads (a later wait for a load
-  // would include these atomics; nothing waits for them).
-  for (int c0 = 0; c0 < pairs; c0 += 64) {
-    const int pr = c0 + lane;
-    const int it = pr / p.kz;
-    if (pr < pairs && tm->g[it] >= 0) counter_add(p.counters + t0 * p.kz + pr, -1);
+}
+
+template <class TL>
+__device__ void lora_gather(const GemvParams& p, char* lds, int t0, int mt, uint32_t tag, int lane) {
+  switch (p.kz) {
+    case 1: lora_gather_kz<TL, 1>(p, lds, t0, mt, tag, lane); break;
+    case 2: lora_gather_kz<TL, 2>(p, lds, t0, mt, tag, lane); break;
+    case 4: lora_gather_kz<TL, 4>(p, lds, t0, mt, tag, lane); break;
+    case 8: lora_gather_kz<TL, 8>(p, lds, t0, mt, tag, lane); break;
+    default: lora_gather_kz<TL, 16>(p, lds, t0, mt, tag, lane); break;
   }
 }
 
@@ -581,8 +771,10 @@ __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMe
     for (int r = 0; r < TL::kRT; ++r)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        b.bf[q][r][h] =
-            load_b8(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row0 + r * 16 + n, 32 * h + 8 * kg, live);
+        // Raw 16 bytes only: the shift/mask (b8_fix) is applied where the
+        // fragments are used, so nothing waits for these loads here.
+        b.bf[q][r][h] = *reinterpret_cast<const uint4*>(
+            b8_at(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row0 + r * 16 + n, 32 * h + 8 * kg, live).src);
   }
 }
 
@@ -592,7 +784,7 @@ template <class TL>
 __device__ __forceinline__ void expand_b_first(const GemvParams& p, const char* lds7, ExpandB<TL>& b, int row0,
                                                int wave, int lane) {
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds7 + LoraLds<TL>::kMeta);
-  while (*reinterpret_cast<const volatile int*>(&tm->ready) == 0) __builtin_amdgcn_s_sleep(1);
+  while (*(const volatile __attribute__((address_space(3))) int*)(&tm->ready) == 0) __builtin_amdgcn_s_sleep(1);
   expand_b_batch<TL>(p, tm, b, wave, row0, lane);
 }
 
@@ -642,7 +834,8 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
           }
 #pragma unroll
           for (int r = 0; r < RT; ++r) {
-            const uint4 bb = cs[r] == s ? b.bf[q][r][h] : make_uint4(0, 0, 0, 0);
+            const B8 b8 = b8_at(p, tm->dboff[d], tm->dstride[d], rk, row0 + r * 16 + n, 32 * h + 8 * kg, true);
+            const uint4 bb = cs[r] == s ? b8_fix(b.bf[q][r][h], b8) : make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < TT; ++t) dacc[r][t] = mfma16(as_bf16x8(zf[t]), as_bf16x8(bb), dacc[r][t]);
           }
@@ -663,7 +856,7 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
 // (p % 8) ^ (row & 7) (conflict-free fragment reads). Scales: position
 // p -> block p / R, row p % R. Positions past the stage and blocks past the
 // wave's range read valid addresses of block kb (their scale is zeroed when
-// used).
+// used). kb must be a valid block.
 template <class TL>
 __device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int row0, int t0, int mt, int kb,
                                             int kend, int lane) {
@@ -698,15 +891,14 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   using TL = Tile<RT, XR>;
   constexpr int TT = TL::kTT;
   constexpr int D = TL::kDepth;
-  constexpr int kBase = kLora ? kWaves - 1 : kWaves;  // waves on the base contraction
-  // The LoRA wave keeps its expand tiles, tile metadata, z and a 4 KiB
-  // partial staging area in its own ring region (extended as needed).
-  constexpr int kLoraExtra = LoraLds<TL>::kBytes > D * TL::kStage ? LoraLds<TL>::kBytes - D * TL::kStage : 0;
+  constexpr int kBase = kLora ? kWaves - 1 : kWaves;  // waves on the base contraction (ring owners)
   static_assert(D * TL::kStage >= 2 * RT * TT * 1024, "base and expand tiles fit a ring region");
-  __shared__ __attribute__((aligned(16))) char ring[kWaves * D * TL::kStage + (kLora ? kLoraExtra : 0)];
+  __shared__ __attribute__((aligned(16))) char ring[kBase * D * TL::kStage];
+  __shared__ __attribute__((aligned(16))) char lora_lds[kLora ? LoraLds<TL>::kBytes : 16];
   __shared__ float table[16];
   __shared__ __attribute__((aligned(16))) uint32_t pt[kExact ? 4 : 256 * kCopies];
-  __shared__ float red[kLora ? kWaves * 192 : 1];
+  __shared__ float red[kLora ? kProd * 192 : 1];
+  __shared__ int prod_done;  // contraction waves that have written their first-unit partials
 
   const int rg = blockIdx.x % p.row_groups;
   const int tile = blockIdx.x / p.row_groups;
@@ -719,7 +911,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   const int kb0 = wave < kBase ? nblk * wave / kBase : 0;
   const int kend = wave < kBase ? nblk * (wave + 1) / kBase : 0;
   const int nst = (kend - kb0 + TL::kSB - 1) / TL::kSB;
-  char* myring = ring + wave * D * TL::kStage;
+  char* myring = ring + wave * D * TL::kStage;  // waves below kBase only
 
   // Codebook (and the LoRA slice bounds) through scalar loads: no vector
   // load may wait behind the copies.
@@ -732,15 +924,40 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     for (int q = 0; q < 4; ++q) bounds[q] = q <= p.slices ? sload(p.slice_offsets, q) : 0;
   }
 
+  // Weight stages (the contraction waves; blocks clamped into range, so all
+  // D stages are always requested). A producing workgroup requests its first
+  // shrink unit's fragments between stage 0 and stage 1 (untracked loads),
+  // so they are not queued behind the whole prologue; they have landed once
+  // stage 1 has, and the contraction waves consume them in their first loop
+  // iteration.
+  Unit un0{};
+  bool has0 = false;
+  UnitFrags pre;
+  TokenMeta tmeta{};
+  uint32_t epoch = 0;
+  if (wave < kBase) {
+    auto stage_kb = [&](int s) { return min(kb0 + s * TL::kSB, nblk - 1); };
+    issue_stage<TL>(p, myring, row0, t0, mt, stage_kb(0), kend, lane);
+    if constexpr (kLora) {
+      has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
+      if (has0) unit_frags<true, kBatch>(p, un0, 0, wave, kProd, lane, pre);
+    }
 #pragma unroll
-  for (int s = 0; s < D; ++s)
-    if (s < nst) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, kb0 + s * TL::kSB, kend, lane);
+    for (int s = 1; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
+  } else if constexpr (kLora) {
+    // The LoRA wave: the epoch and its tile's token metadata.
+    epoch = __hip_atomic_load(p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    tmeta = token_meta(p, t0, mt, lane);
+    has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
+  }
 
   if (threadIdx.x == 0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) table[i] = cb[i];
-    if constexpr (kLora)
-      reinterpret_cast<TileMeta*>(ring + kBase * D * TL::kStage + LoraLds<TL>::kMeta)->ready = 0;
+    if constexpr (kLora) {
+      reinterpret_cast<TileMeta*>(lora_lds + LoraLds<TL>::kMeta)->ready = 0;
+      prod_done = 0;
+    }
   }
   if constexpr (!kExact) {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -755,7 +972,16 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   barrier_only();
   const uint32_t* ptl = pt + (lane % kCopies);
-  if constexpr (kLora) produce_units(p, red, wave, lane, wave == kBase);
+  // The LoRA wave: tile metadata, then the first unit (published as soon as
+  // the contraction waves have counted in), the other units, then z.
+  if constexpr (kLora) {
+    if (wave == kBase) {
+      const uint32_t tag = __builtin_amdgcn_readfirstlane(epoch) + 1u;
+      lora_meta<TL>(lora_lds, tmeta, lane);
+      if (has0) publish_first_unit(p, red, &prod_done, un0, tag, lane);
+      produce_other_units(p, tag, lane);
+    }
+  }
 
   f32x4 acc[RT][TT];
 #pragma unroll
@@ -781,6 +1007,11 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       wait_stages<TL>(min(D - 2, nst - 2 - s));
       read_frags<TL>(nxt, ring_base + ((s + 1) % D) * TL::kStage, n, g);
     }
+    // Stage 1 has landed, so have the first unit's fragments (requested
+    // before it).
+    if constexpr (kLora) {
+      if (s == 0 && more && has0) first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
+    }
     if (s + D < nst)
       issue_stage<TL>(p, myring + (s % D) * TL::kStage, row0, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
     const int kb = kb0 + s * TL::kSB;
@@ -797,11 +1028,17 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   // wave adds its share of the expand into a second tile set after its base
   // tiles.
   constexpr int kTiles = RT * TT;
-  char* lora7 = ring + kBase * D * TL::kStage;
+  char* lora7 = lora_lds;
   ExpandB<TL> eb;
+  uint32_t departed = 0;
   if (kLora && wave == kBase) {
-    lora_prepare<TL>(p, myring, t0, mt, lane);
+    lora_gather<TL>(p, lora7, t0, mt, __builtin_amdgcn_readfirstlane(epoch) + 1u, lane);
+    departed = depart_issue(p, lane);  // after the last partial load: nothing waits for it until the end
   } else {
+    wait_vm<0>();  // stages past the wave's blocks (short K) may still be landing in the ring
+    if constexpr (kLora) {
+      if (has0 && nst < 2) first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
+    }
     f32x4* red = reinterpret_cast<f32x4*>(myring);
 #pragma unroll
     for (int r = 0; r < RT; ++r)
@@ -812,8 +1049,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     if constexpr (kLora) expand_b_first<TL>(p, lora7, eb, row0, wave, lane);
   }
   auto delta_tiles = [&](int w) { return reinterpret_cast<f32x4*>(ring + w * D * TL::kStage + kTiles * 1024); };
-  // LDS-only barriers: a full fence here would also wait for the LoRA wave's
-  // counter releases and the early B loads.
+  // LDS-only barriers: a full fence here would also wait for the early B
+  // loads.
   if constexpr (kLora) {
     lds_barrier();  // z and the tile metadata are in LDS
     if (wave < kBase) expand_mfma<TL>(p, lora7, eb, bounds, delta_tiles(wave), row0, wave, lane);
@@ -854,6 +1091,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       }
     }
   }
+  if (kLora && wave == kBase) depart_finish(p, departed, __builtin_amdgcn_readfirstlane(epoch), lane);
 }
 
 template <int RT, int XR, bool kLora>
@@ -868,7 +1106,6 @@ void launch_tile(bool exact, bool lora, dim3 grid, hipStream_t s, const GemvPara
   else launch_exact<RT, XR, false>(exact, grid, s, p);
 }
 
-constexpr int64_t kCounterOffset = 256;  // counters follow the status words in the control header
 
 int device_cus() {
   static int cached[64] = {0};
@@ -895,6 +1132,15 @@ struct GemvPlan {
 // Shrink units: m tokens x kz k-slices, kz chosen so that m * kz is about
 // min(grid, CUs) (one unit per producing workgroup when m allows) and a
 // consumer's partial reads fit one batch.
+// Control header layout: epoch, status, eight group arrival counts (128
+// bytes apart), the group total, then the tagged shrink partials (at most
+// 64 tokens x 192 values x 8 bytes).
+constexpr int64_t kEpochOffset = 0;
+constexpr int64_t kStatusOffset = 8;
+constexpr int64_t kGroupsOffset = 128;
+constexpr int64_t kTotalOffset = kGroupsOffset + 8 * 128;
+constexpr int64_t kPartialsOffset = 2048;
+
 GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
   GemvPlan pl;
   pl.rows = m > 32 ? 32 : 16;
@@ -906,10 +1152,13 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
   // 1024-value batch where the shape allows, and at most half of the
   // workgroups producing (production delays their contraction).
   const int64_t tile_tokens = std::min<int64_t>(m, 32);
-  const int64_t kz = std::max<int64_t>(
+  int64_t kz = std::max<int64_t>(
       1, std::min<int64_t>({nblk, cap / (2 * m), 16, 1024 / std::max<int64_t>(1, tile_tokens * zw)}));
+  while (kz & (kz - 1)) kz &= kz - 1;  // a power of two (the consumer sums the slices unrolled)
   pl.kz_len = int((nblk + kz - 1) / kz) * 64;
-  pl.kz = int((k + pl.kz_len - 1) / pl.kz_len);
+  pl.kz = int(kz);  // trailing slices may be empty (their partials are zero)
+  // The consumer holds 16 entries per lane and batch: one token's kz * zw
+  // entries must fit 1024 (kz > 1 only when that holds; zw <= 192 at kz = 1).
   pl.units = int(m) * pl.kz;
   pl.producers = int(cap);
   return pl;
@@ -917,10 +1166,7 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
 
 }  // namespace
 
-int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank) {
-  const GemvPlan pl = gemv_plan(m, n, k, 1 << 20, slices * max_rank);  // upper bound over CU counts
-  return kWorkspaceHeader + (int64_t(pl.units) * slices * max_rank * 4 + 255) / 256 * 256;
-}
+int64_t gemv_workspace_bytes(int64_t, int64_t, int64_t, int, int) { return kWorkspaceHeader; }
 
 // Fused NF4 + multi-LoRA linear for 1..64 tokens with fp32 block scales.
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
@@ -944,10 +1190,11 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   p.y_stride = y_stride;
   p.row_groups = pl.row_groups;
   if (lora) {
-    const int64_t need = kWorkspaceHeader + int64_t(pl.units) * lora->num_slices * lora->max_rank * 4;
-    LF_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %lld bytes", (long long)need);
+    LF_REQUIRE(workspace && workspace_bytes >= kWorkspaceHeader, "workspace too small: need %lld bytes",
+               (long long)kWorkspaceHeader);
+    LF_REQUIRE(kPartialsOffset + int64_t(pl.units) * lora->num_slices * lora->max_rank * 8 <= kWorkspaceHeader,
+               "shrink partials exceed the control header");
     LF_REQUIRE(aligned16(workspace), "workspace must be 16-byte aligned");
-    LF_REQUIRE(kCounterOffset + 4 * int64_t(pl.units) <= kWorkspaceHeader, "too many shrink units");
     p.a_store = lora->a_store;
     p.a_offsets = lora->a_offsets;
     p.b_store = lora->b_store;
@@ -963,12 +1210,13 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
     p.units = pl.units;
     p.kz = pl.kz;
     p.kz_len = pl.kz_len;
-    p.consumers = pl.row_groups;
     p.producers = pl.producers;
     char* ws = static_cast<char*>(workspace);
-    p.status = reinterpret_cast<int*>(ws + 8);
-    p.counters = reinterpret_cast<int*>(ws + kCounterOffset);
-    p.zp = reinterpret_cast<float*>(ws + kWorkspaceHeader);
+    p.epoch = reinterpret_cast<uint32_t*>(ws + kEpochOffset);
+    p.status = reinterpret_cast<int*>(ws + kStatusOffset);
+    p.groups = reinterpret_cast<uint32_t*>(ws + kGroupsOffset);
+    p.total = reinterpret_cast<uint32_t*>(ws + kTotalOffset);
+    p.zp = reinterpret_cast<uint64_t*>(ws + kPartialsOffset);
   }
   const dim3 grid(unsigned(pl.grid));
   auto s = static_cast<hipStream_t>(stream);

@@ -408,7 +408,7 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.lscales = lora->scales;
     p.token_slots = lora->token_slots;
     p.slice_offsets = lora->slice_offsets;
-    p.zpad = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + kWorkspaceHeader);  // after the decode counters
+    p.zpad = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + kWorkspaceHeader);  // after the decode header
     hipLaunchKernelGGL(prefill_shrink_kernel, dim3(unsigned((m + 15) / 16)), dim3(kThreads), 0, s, p);
     LF_HIP(hipGetLastError());
   }

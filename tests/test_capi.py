@@ -51,6 +51,6 @@ def test_workspace_size_is_host_arithmetic():
     small = lib.lf_nf4_lora_workspace_size(1, 4096, 4096, 1, 16)
     big = lib.lf_nf4_lora_workspace_size(64, 4096, 4096, 1, 16)
     prefill = lib.lf_nf4_lora_workspace_size(2048, 11008, 4096, 1, 32)
-    assert 65536 < small <= big  # the 64 KiB control header comes first
-    assert prefill >= 65536 + 2048 * 64 * 2  # prefill z rows sit after that header
+    assert small == big == 131072  # decode: the 128 KiB control header (tagged shrink partials inside)
+    assert prefill >= 131072 + 2048 * 64 * 2  # prefill z rows sit after that header
     assert lib.lf_nf4_lora_workspace_size(-1, 64, 64, 1, 1) == -1
