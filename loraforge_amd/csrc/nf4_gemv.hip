@@ -436,14 +436,60 @@ __device__ __forceinline__ void unit_frags(const GemvParams& p, const Unit& un, 
   }
 }
 
-// Ties every fragment register to a wait already made (no use may be
-// scheduled above it).
-__device__ __forceinline__ void tie_frags(UnitFrags& f) {
+// The first batch of a workgroup's first unit, requested in the prologue
+// (untracked loads). x is compact: lane 4 i + g (i < kBatch, g < 4) holds
+// the 16 bytes of k-group g of step st0 + i * kProd, one gathered load; the
+// MFMA layout (row 0 only) is formed when used.
+struct FirstFrags {
+  u32x4 xc;
+  u32x4 av[kBatch];
+};
+
+__device__ __forceinline__ void first_frags(const GemvParams& p, const Unit& un, int st0, int lane, FirstFrags& f) {
+  const int jn = lane & 15;
+  const int kg = lane >> 4;
+  {
+    const int i = min(lane >> 2, kBatch - 1);
+    const int st = st0 + i * kProd;
+    const int sc = st < un.steps ? st : max(un.steps - 1, 0);
+    const uint16_t* xp = p.x + int64_t(un.t) * p.x_stride + un.kb + 32 * sc + 8 * (lane & 3);
+    f.xc = global_load128_untracked_masked(xp, (uint64_t(1) << (4 * kBatch)) - 1);
+  }
+  const int j = jn;
+  const uint16_t* arow = p.a_store + un.aoff + int64_t(j < un.rows ? j : un.rows - 1) * p.k + un.kb + 8 * kg;
 #pragma unroll
   for (int i = 0; i < kBatch; ++i) {
-    tie(f.xv[i]);
-    tie(f.av[i]);
+    const int st = st0 + i * kProd;
+    const int sc = st < un.steps ? st : max(un.steps - 1, 0);
+    f.av[i] = global_load128_untracked(arow + 32 * sc);
   }
+}
+
+// Ties every fragment register to a wait already made (no use may be
+// scheduled above it).
+__device__ __forceinline__ void tie_frags(FirstFrags& f) {
+  tie(f.xc);
+#pragma unroll
+  for (int i = 0; i < kBatch; ++i) tie(f.av[i]);
+}
+
+// MFMAs of the first batch: step i's x fragment for lane (row jn, k-group
+// kg) comes from lane 4 i + kg of xc (row 0 only; other rows zero).
+__device__ __forceinline__ f32x4 first_mfma(const FirstFrags& f, const Unit& un, int st0, int lane, f32x4 c) {
+  const int kg = lane >> 4;
+  const bool row0 = (lane & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < kBatch; ++i) {
+    const int src = (4 * i + kg) << 2;
+    u32x4 x;
+    x.x = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(f.xc.x)));
+    x.y = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(f.xc.y)));
+    x.z = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(f.xc.z)));
+    x.w = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(f.xc.w)));
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    c = mfma16(vec_bf16x8(row0 && st0 + i * kProd < un.steps ? x : zero), vec_bf16x8(f.av[i]), c);
+  }
+  return c;
 }
 
 template <int NB>
@@ -460,7 +506,7 @@ __device__ __forceinline__ f32x4 unit_mfma(const UnitFragsN<NB>& f, const Unit& 
 // higher j are never read). pre holds the first batch of row group 0 (already
 // landed); anything beyond it is loaded here. Then the wave counts itself
 // in (LDS) so the LoRA wave can publish without a workgroup barrier.
-__device__ void first_unit_partials(const GemvParams& p, const Unit& un, UnitFrags& pre, float* red, int* done,
+__device__ void first_unit_partials(const GemvParams& p, const Unit& un, FirstFrags& pre, float* red, int* done,
                                     int wave, int lane) {
   tie_frags(pre);
   const int jn = lane & 15;
@@ -469,7 +515,7 @@ __device__ void first_unit_partials(const GemvParams& p, const Unit& un, UnitFra
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
     int st0 = wave;
     if (j0 == 0) {
-      c = unit_mfma(pre, un, st0, kProd, c);
+      c = first_mfma(pre, un, st0, lane, c);
       st0 += kBatch * kProd;
     }
     // Anything beyond the first batch (ranks above 16, long slices) in small
@@ -753,7 +799,7 @@ constexpr int kExpandWaves = kWaves - 1;
 
 template <class TL>
 struct ExpandB {
-  uint4 bf[4][TL::kRT][2];
+  uint4 bf[4][TL::kRT];  // ranks 0..31 (ranks 32..63 are loaded where used)
 };
 
 template <class TL>
@@ -769,12 +815,10 @@ __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMe
     const int dd = live ? d : 0;
 #pragma unroll
     for (int r = 0; r < TL::kRT; ++r)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        // Raw 16 bytes only: the shift/mask (b8_fix) is applied where the
-        // fragments are used, so nothing waits for these loads here.
-        b.bf[q][r][h] = *reinterpret_cast<const uint4*>(
-            b8_at(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row0 + r * 16 + n, 32 * h + 8 * kg, live).src);
+      // Raw 16 bytes only: the shift/mask (b8_fix) is applied where the
+      // fragments are used, so nothing waits for these loads here.
+      b.bf[q][r] = *reinterpret_cast<const uint4*>(
+          b8_at(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row0 + r * 16 + n, 8 * kg, live).src);
   }
 }
 
@@ -789,8 +833,8 @@ __device__ __forceinline__ void expand_b_first(const GemvParams& p, const char* 
 }
 
 template <class TL>
-__device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& b, const int (&bounds)[4], f32x4* out,
-                            int row0, int wave, int lane) {
+__device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& b, const int (&bounds)[4],
+                            f32x4 (&dacc)[TL::kRT][TL::kTT], int row0, int wave, int lane) {
   using L = LoraLds<TL>;
   constexpr int RT = TL::kRT;
   constexpr int TT = TL::kTT;
@@ -798,7 +842,6 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
   const uint16_t* zl = reinterpret_cast<const uint16_t*>(lds7 + L::kZ);
   const int n = lane & 15;
   const int kg = lane >> 4;
-  f32x4 dacc[RT][TT];
 #pragma unroll
   for (int r = 0; r < RT; ++r)
 #pragma unroll
@@ -835,7 +878,8 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
 #pragma unroll
           for (int r = 0; r < RT; ++r) {
             const B8 b8 = b8_at(p, tm->dboff[d], tm->dstride[d], rk, row0 + r * 16 + n, 32 * h + 8 * kg, true);
-            const uint4 bb = cs[r] == s ? b8_fix(b.bf[q][r][h], b8) : make_uint4(0, 0, 0, 0);
+            const uint4 raw = h == 0 ? b.bf[q][r] : *reinterpret_cast<const uint4*>(b8.src);
+            const uint4 bb = cs[r] == s ? b8_fix(raw, b8) : make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < TT; ++t) dacc[r][t] = mfma16(as_bf16x8(zf[t]), as_bf16x8(bb), dacc[r][t]);
           }
@@ -843,10 +887,6 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
       }
     }
   }
-#pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int t = 0; t < TT; ++t) out[(r * TT + t) * 64 + lane] = dacc[r][t];
 }
 
 // Copies of one stage (kSB blocks starting at block kb) into a ring slot.
@@ -932,7 +972,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   // iteration.
   Unit un0{};
   bool has0 = false;
-  UnitFrags pre;
+  FirstFrags pre;
   TokenMeta tmeta{};
   uint32_t epoch = 0;
   if (wave < kBase) {
@@ -940,7 +980,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     issue_stage<TL>(p, myring, row0, t0, mt, stage_kb(0), kend, lane);
     if constexpr (kLora) {
       has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
-      if (has0) unit_frags<true, kBatch>(p, un0, 0, wave, kProd, lane, pre);
+      if (has0) first_frags(p, un0, wave, lane, pre);
     }
 #pragma unroll
     for (int s = 1; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
@@ -996,12 +1036,20 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   // and contracted; the slot of stage s is refilled as soon as its fragments
   // are in registers.
   Frags<TL> cur, nxt;
+  ExpandB<TL> eb;
+  static_assert((D - 1) * TL::kDma + kBatch + 1 < 64, "vmcnt range");
   if (nst > 0) {
-    wait_stages<TL>(min(D - 1, nst - 1));
+    // A producing wave requested its unit fragments between stage 0 and
+    // stage 1: stage 0 has landed once only those and the later stages are
+    // outstanding.
+    if (kLora && has0 && nst >= D) wait_vm<(D - 1) * TL::kDma + (kLora ? kBatch + 1 : 0)>();
+    else wait_stages<TL>(min(D - 1, nst - 1));
     read_frags<TL>(cur, ring_base, n, g);
     settle(cur);
   }
-  for (int s = 0; s < nst; ++s) {
+  // One ring stage: read the next stage's fragments, refill, contract this
+  // one.
+  auto step = [&](int s, bool first) {
     const bool more = s + 1 < nst;
     if (more) {
       wait_stages<TL>(min(D - 2, nst - 2 - s));
@@ -1010,17 +1058,19 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     // Stage 1 has landed, so have the first unit's fragments (requested
     // before it).
     if constexpr (kLora) {
-      if (s == 0 && more && has0) first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
+      if (first && more && has0) first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
     }
     if (s + D < nst)
       issue_stage<TL>(p, myring + (s % D) * TL::kStage, row0, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
-    const int kb = kb0 + s * TL::kSB;
-    contract<TL, kExact>(cur, kb, kend, acc, table, ptl);
+    contract<TL, kExact>(cur, kb0 + s * TL::kSB, kend, acc, table, ptl);
     if (more) {
       settle(nxt);
       cur = nxt;
     }
-  }
+  };
+  // Stage 0 apart, so that the unit fragments are not live in the loop.
+  if (nst > 0) step(0, true);
+  for (int s = 1; s < nst; ++s) step(s, false);
 
   // Sum the waves' partial tiles: wave w writes its tiles into its own ring
   // (all of its copies have landed), then tile c = wave is summed by wave c.
@@ -1029,31 +1079,44 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   // tiles.
   constexpr int kTiles = RT * TT;
   char* lora7 = lora_lds;
-  ExpandB<TL> eb;
   uint32_t departed = 0;
-  if (kLora && wave == kBase) {
-    lora_gather<TL>(p, lora7, t0, mt, __builtin_amdgcn_readfirstlane(epoch) + 1u, lane);
-    departed = depart_issue(p, lane);  // after the last partial load: nothing waits for it until the end
+  auto delta_tiles = [&](int w) { return reinterpret_cast<f32x4*>(ring + w * D * TL::kStage + kTiles * 1024); };
+  if constexpr (kLora) {
+    // The LoRA wave finishes z while the others request their first B
+    // fragments; after the barrier (LDS only: a full fence would wait for the
+    // B loads) the contraction waves compute the expand in registers.
+    f32x4 dacc[RT][TT];
+    if (wave == kBase) {
+      lora_gather<TL>(p, lora7, t0, mt, __builtin_amdgcn_readfirstlane(epoch) + 1u, lane);
+      departed = depart_issue(p, lane);  // after the last partial load: nothing waits for it until the end
+    } else {
+      if (has0 && nst < 2) {
+        wait_vm<0>();
+        first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
+      }
+      expand_b_first<TL>(p, lora7, eb, row0, wave, lane);
+    }
+    lds_barrier();  // z and the tile metadata are in LDS
+    if (wave < kBase) expand_mfma<TL>(p, lora7, eb, bounds, dacc, row0, wave, lane);
+    if (wave < kBase) {
+      wait_vm<0>();  // stages past the wave's blocks (short K) may still be landing in the ring
+      f32x4* base_tiles = reinterpret_cast<f32x4*>(myring);
+      f32x4* dt = delta_tiles(wave);
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          base_tiles[(r * TT + t) * 64 + lane] = acc[r][t];
+          dt[(r * TT + t) * 64 + lane] = dacc[r][t];
+        }
+    }
   } else {
     wait_vm<0>();  // stages past the wave's blocks (short K) may still be landing in the ring
-    if constexpr (kLora) {
-      if (has0 && nst < 2) first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
-    }
-    f32x4* red = reinterpret_cast<f32x4*>(myring);
+    f32x4* base_tiles = reinterpret_cast<f32x4*>(myring);
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int t = 0; t < TT; ++t) red[(r * TT + t) * 64 + lane] = acc[r][t];
-    // After the ring stores: the compiler waits for every outstanding load
-    // before storing into the ring, which would include these.
-    if constexpr (kLora) expand_b_first<TL>(p, lora7, eb, row0, wave, lane);
-  }
-  auto delta_tiles = [&](int w) { return reinterpret_cast<f32x4*>(ring + w * D * TL::kStage + kTiles * 1024); };
-  // LDS-only barriers: a full fence here would also wait for the early B
-  // loads.
-  if constexpr (kLora) {
-    lds_barrier();  // z and the tile metadata are in LDS
-    if (wave < kBase) expand_mfma<TL>(p, lora7, eb, bounds, delta_tiles(wave), row0, wave, lane);
+      for (int t = 0; t < TT; ++t) base_tiles[(r * TT + t) * 64 + lane] = acc[r][t];
   }
   lds_barrier();
   if (wave < kTiles) {
