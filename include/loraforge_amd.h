@@ -127,18 +127,21 @@ typedef struct lf_lora {
  * first 128 KiB are the decode kernel's control header (a launch word, a
  * status word and the shrink partials, each tagged with the call that wrote
  * it); it must be zero before the first call and is never reset between
- * calls. Decode and prefill calls may share one workspace; calls that share
- * one workspace must not overlap in time. */
+ * calls. A prefill call uses the rest for its z rows and, for a double-quant
+ * weight, the rebuilt fp32 block scales. Decode and prefill calls may share
+ * one workspace; calls that share one workspace must not overlap in time. */
 int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices, int32_t max_rank);
 
 /* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);
  * y [m, N] bf16 with row stride y_stride; bias bf16 [N] or NULL;
  * lora NULL for the base linear alone. M <= 64 runs the decode kernel
- * (fp32 block scales required), M > 64 the prefill GEMM.
- * flags: LF_EXACT_WEIGHTS makes the decode kernel multiply bf16_rne(code *
- * scale) weights (the reference's dequantised W, bit for bit); by default it
- * contracts bf16(code) and applies each fp32 block scale to the block's MFMA
- * sum. The prefill GEMM always uses the exact weights. */
+ * (fp32 block scales required), M > 64 the prefill GEMM, which multiplies
+ * the reference's dequantised weights bf16_rne(code * scale) bit for bit and
+ * takes fp32 block scales or a double-quant state (rebuilt into the
+ * workspace first; the workspace is then required even without LoRA).
+ * flags: LF_EXACT_WEIGHTS makes the decode kernel multiply the same exact
+ * weights; by default it contracts bf16(code) and applies each fp32 block
+ * scale to the block's MFMA sum. The prefill GEMM ignores the flag. */
 #define LF_EXACT_WEIGHTS 1
 int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* weight,
                        const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,

@@ -41,10 +41,10 @@ HIP_FLAGS = [
 ]
 
 
-# Sources whose kernels must not use scratch: the decode kernel issues global
-# loads the compiler does not track (waited for explicitly), and a register
-# spill of such a result would store it before the load has returned.
-NO_SCRATCH = {"nf4_gemv.hip"}
+# Sources whose kernels must not use scratch: the decode and prefill kernels
+# issue loads the compiler does not track (waited for explicitly), and a
+# register spill of such a result would store it before the load returned.
+NO_SCRATCH = {"nf4_gemv.hip", "nf4_lora_prefill.hip"}
 
 
 def hipcc() -> str:

@@ -1,0 +1,82 @@
+// Building blocks of the direct-copy LDS pipelines (decode and prefill
+// kernels): global -> LDS copies, explicit vmcnt waits, LDS reads the
+// compiler does not track, and workgroup barriers that wait for LDS only.
+//
+// Why untracked reads: while global -> LDS copies are in flight the compiler
+// waits for every outstanding memory operation before any LDS read it
+// tracks (it cannot tell which LDS bytes a copy writes). The kernels know
+// which copies a read depends on and wait for exactly those (wait_vm), then
+// tie the read results to the wait so no use is scheduled above it.
+#pragma once
+
+#include "common.h"
+
+namespace lf {
+
+template <class T>
+__device__ __forceinline__ T sload(const T* base, int idx) {
+  typedef const __attribute__((address_space(4))) T* ConstPtr;
+  return ((ConstPtr)base)[idx];
+}
+
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// Workgroup barrier after this wave's LDS accesses completed (lgkmcnt(0)),
+// without waiting for its global memory operations.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  barrier_only();
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0xF << 8) | (7 << 4));  // vmcnt(N) only
+}
+
+__device__ __forceinline__ void copy16(const void* src, char* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void copy4(const void* src, char* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+// LDS reads the compiler does not track (results valid after an explicit
+// lgkmcnt wait and tie).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16x8 vec_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ u32x2 lds_read64(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ u32x4 lds_read128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ float lds_read32f(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// Ties a value to the wait made before it: uses cannot be scheduled above.
+template <class T>
+__device__ __forceinline__ void tie(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
+__device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+}  // namespace lf

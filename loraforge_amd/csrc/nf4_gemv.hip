@@ -19,6 +19,7 @@
 // read from HBM once).
 #include <algorithm>
 
+#include "lds_pipeline.h"
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
 
@@ -87,27 +88,6 @@ struct GemvParams {
 
 constexpr int kSpinLimit = 1 << 20;
 
-template <class T>
-__device__ __forceinline__ T sload(const T* base, int idx) {
-  typedef const __attribute__((address_space(4))) T* ConstPtr;
-  return ((ConstPtr)base)[idx];
-}
-
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
-
-// Workgroup barrier after this wave's LDS accesses completed (lgkmcnt(0)),
-// without waiting for its global memory operations.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  barrier_only();
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0xF << 8) | (7 << 4));  // vmcnt(N) only
-}
-
 // vmcnt(n) for n = c * kDma, c < kDepth (runtime c).
 template <class TL>
 __device__ __forceinline__ void wait_stages(int c) {
@@ -121,45 +101,6 @@ __device__ __forceinline__ void wait_stages(int c) {
     case 6: wait_vm<(TL::kDepth > 6 ? 6 : 0) * TL::kDma>(); break;
     default: wait_vm<(TL::kDepth > 7 ? 7 : 0) * TL::kDma>(); break;
   }
-}
-
-__device__ __forceinline__ void copy16(const void* src, char* lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-__device__ __forceinline__ void copy4(const void* src, char* lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
-}
-
-// LDS reads the compiler does not track: the ring is written by direct copies
-// whose completion each wave checks itself (vmcnt), so no compiler wait may
-// be attached to these reads. Results are valid after lds_wait().
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ bf16x8 vec_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
-__device__ __forceinline__ u32x2 lds_read64(uint32_t addr) {
-  u32x2 v;
-  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
-__device__ __forceinline__ u32x4 lds_read128(uint32_t addr) {
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
-__device__ __forceinline__ float lds_read32f(uint32_t addr) {
-  float v;
-  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
-}
-
-// lgkmcnt(0), then every value read by the untracked LDS reads is tied to
-// the wait so that no use can be scheduled above it.
-template <class T>
-__device__ __forceinline__ void tie(T& v) {
-  asm volatile("" : "+v"(v));
 }
 
 template <int kC>

@@ -8,19 +8,17 @@
 // Two launches on the caller's stream:
 //  1. shrink: per 16-token block and distinct slot, z = bf16(x A_g^T) on
 //     MFMA into a slice-padded workspace zpad[m][s*64 + j] (zeros past r).
-//  2. GEMM: workgroup tile 256 tokens x 128 output features, BK = 64 (one
-//     NF4 block per W row per k-step). x tiles go global -> registers -> LDS;
-//     W tiles are 16 packed bytes per thread, decoded in registers (codebook
-//     in LDS) to exact bf16 and written to LDS; four waves (2 x 2) each own
-//     128 x 64 outputs as 8 x 4 fragments of v_mfma_f32_16x16x32_bf16.
-//     LDS rows are 128 B with a 16-byte-unit XOR swizzle (unit ^ row % 8).
-//     Epilogue: round, bias, then per slice the tile's z rows are staged in
-//     LDS once and, for every distinct slot in the tile, a second MFMA pass
-//     z x B_g^T over the 16-row blocks holding its tokens gives the LoRA
-//     delta, applied with the reference's two bf16 roundings to the rows
-//     routed to that slot.
-//  Tile order puts M-tile b % mtiles on consecutive block ids, so with 8
-//  M-tiles each XCD (block id % 8) keeps one 2 MiB x panel in its L2.
+//  2. GEMM (wide::gemm_kernel): workgroup tile 256 tokens x 192 output
+//     features; x streamed by direct global -> LDS copies, W decoded once per
+//     tile to the reference's exact weights bf16_rne(code * scale) (fp32 or
+//     double-quant block scales) into LDS, contracted on
+//     v_mfma_f32_16x16x32_bf16. LDS rows are 128 B with a 16-byte-unit XOR
+//     swizzle (unit ^ row % 8). Epilogue: round, bias, then per slice the
+//     tile's z rows are staged in LDS once and, for every distinct slot in
+//     the tile, a second MFMA pass z x B_g^T over the 16-row blocks holding
+//     its tokens gives the LoRA delta, applied with the reference's two bf16
+//     roundings to the rows routed to that slot.
+#include "lds_pipeline.h"
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
 
@@ -29,7 +27,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kBM = 256;
-constexpr int kBN = 128;
 constexpr int kBK = 64;
 constexpr int kZSlice = 64;  // zpad columns per slice
 
@@ -160,9 +157,7 @@ __global__ __launch_bounds__(kThreads) void prefill_shrink_kernel(PrefillParams 
   }
 }
 
-// ---------------------------------------------------------------------------
-// 2. GEMM + epilogue.
-// ---------------------------------------------------------------------------
+// LoRA B row segment [kk, kk + 8) of a row of length br (zeros past br).
 __device__ __forceinline__ uint4 load_b8(const uint16_t* brow, int kk, int br) {
   if (kk + 8 <= br) return *reinterpret_cast<const uint4*>(brow + kk);
   uint32_t h[8];
@@ -171,95 +166,335 @@ __device__ __forceinline__ uint4 load_b8(const uint16_t* brow, int kk, int br) {
   return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
 }
 
-template <bool kDouble, bool kLora>
-__global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(PrefillParams p) {
-  __shared__ uint4 xs[kBM * 8];
-  __shared__ uint4 ws[kBN * 8];
-  __shared__ float table[16];
-  __shared__ float code2[kDouble ? 256 : 1];
-  __shared__ __attribute__((aligned(16))) int tslot[kBM];
-  __shared__ int list[kMaxList + 1];
+// ---------------------------------------------------------------------------
+// 2. GEMM + epilogue: 512 threads (two waves per SIMD), tile 256 tokens x
+// 192 output features, BK = 64 (one NF4 block per W row).
+//
+// Per k-step a workgroup
+//  - copies the x tile two steps ahead straight into a three-stage LDS ring
+//    (global -> LDS, 16-byte XOR swizzle), four copies per wave;
+//  - loads the packed W bytes and block scales two steps ahead into
+//    registers (three dwords, 24 elements, per lane), and decodes the step
+//    ahead to exact bf16_rne(code * scale) into the other half of a
+//    two-stage decoded-W buffer, so each weight is decoded once per tile;
+//  - contracts the current stage: waves (2 x 4) own 128 x 48 outputs
+//    (8 x 3 fragments of v_mfma_f32_16x16x32_bf16), the decode work of the
+//    next step interleaved with these MFMAs;
+//  - waits for the next x copies and meets the other waves at one barrier.
+// Tile order keeps M-tile b % mtiles on consecutive block ids (one 2 MiB x
+// panel per XCD L2 with 8 M-tiles).
+// ---------------------------------------------------------------------------
+namespace wide {
+
+constexpr int kThreads = 512;
+constexpr int kBM = 256;
+constexpr int kBN = 192;
+constexpr int kXD = 3;                   // x ring depth
+constexpr int kXBytes = kBM * 128;       // one x stage: 256 rows x 64 bf16
+constexpr int kWBytes = kBN * 128;       // one decoded-W stage: 192 rows x 64 bf16
+constexpr int kXCopies = kXBytes / 1024 / (kThreads / 64);  // 16-byte copies per lane and stage
+constexpr int kDw = kBN * 8 / kThreads;  // packed W dwords per lane and stage
+constexpr int kJ = 3;                    // 16-column fragments per wave
+static_assert(kBN * 8 % kThreads == 0 && kXBytes % (1024 * (kThreads / 64)) == 0, "tile split");
+static_assert(kXD * kXBytes + 2 * kWBytes + 2048 <= 160 * 1024, "LDS budget");
+
+// Packed W dwords and fp32 block scales of one k-step, loaded without
+// compiler tracking (the x copies in flight would otherwise make every use of
+// them wait for all outstanding memory operations).
+struct Packed {
+  uint32_t q[kDw];
+  uint32_t s[kDw];  // fp32 scale bits
+  static constexpr int kLoads = 2 * kDw;
+};
+
+__device__ __forceinline__ uint32_t gload32(const void* base, uint32_t voff) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(voff), "s"(base) : "memory");
+  return v;
+}
+
+// Per-lane W addressing: lane dword i covers tile row (tid >> 3) + 64 i,
+// elements 8 (tid & 7) .. + 8 of the k-step. Rows past N are clamped (their
+// results are never stored).
+struct WLane {
+  uint32_t qoff[kDw];  // byte offset of the dword at k-step 0
+  uint32_t soff[kDw];  // byte offset of the row's block scale at k-step 0
+};
+
+__device__ __forceinline__ void issue_w(const PrefillParams& p, int kt, const WLane& wl, Packed& w) {
+  const uint8_t* qb = p.q + int64_t(kt) * 32;
+#pragma unroll
+  for (int i = 0; i < kDw; ++i) w.q[i] = gload32(qb, wl.qoff[i]);
+  const float* sb = p.src.scales + kt;
+#pragma unroll
+  for (int i = 0; i < kDw; ++i) w.s[i] = gload32(sb, wl.soff[i]);
+}
+
+__device__ __forceinline__ void tie_w(Packed& w) {
+#pragma unroll
+  for (int i = 0; i < kDw; ++i) {
+    tie(w.q[i]);
+    tie(w.s[i]);
+  }
+}
+
+// LDS accesses the compiler does not track, with immediate offsets.
+template <int kOff>
+__device__ __forceinline__ u32x4 ldsr128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(kOff));
+  return v;
+}
+template <int kOff>
+__device__ __forceinline__ void ldsw128(uint32_t addr, const u32x4& v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "i"(kOff) : "memory");
+}
+
+// Decode of one loaded step into a decoded-W stage, in two halves: the
+// codebook lookups of all dwords, then the scaling, rounding and the stores.
+// The codebook sits 256-byte aligned in LDS, so a lookup address is the table
+// address with its low byte replaced by 4 * nibble (one byte permute).
+struct Looked {
+  float v[kDw][8];
+};
+
+// Lookup addresses: byte b of `even` / `odd` holds 4 * the high / low nibble
+// of packed byte b.
+struct LookAddr {
+  uint32_t a[kDw][8];
+};
+
+__device__ __forceinline__ void lookup_addresses(const Packed& w, uint32_t table_addr, LookAddr& la) {
+#pragma unroll
+  for (int i = 0; i < kDw; ++i) {
+    const uint32_t d = w.q[i];
+    const uint32_t even = (d >> 2) & 0x3c3c3c3cu;
+    const uint32_t odd = (d << 2) & 0x3c3c3c3cu;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      // Byte 0 from byte b of the first operand, bytes 1..3 from the table address.
+      const uint32_t sel = 0x03020100u | (4u + b);
+      la.a[i][2 * b] = __builtin_amdgcn_perm(even, table_addr, sel);
+      la.a[i][2 * b + 1] = __builtin_amdgcn_perm(odd, table_addr, sel);
+    }
+  }
+}
+
+// The 8 lookups of dword i.
+__device__ __forceinline__ void lookup_dword(const LookAddr& la, int i, Looked& lk) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) lk.v[i][e] = lds_read32f(la.a[i][e]);
+}
+
+__device__ __forceinline__ void tie_lookups(Looked& lk) {
+#pragma unroll
+  for (int i = 0; i < kDw; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tie(lk.v[i][e]);
+}
+
+// bf16_rne(code * scale) of dword i's 8 elements, stored at row offset i * 64.
+__device__ __forceinline__ void decode_store(const Packed& w, const Looked& lk, uint32_t dst) {
+#pragma unroll
+  for (int i = 0; i < kDw; ++i) {
+    const float scale = __uint_as_float(w.s[i]);
+    u32x4 r;
+    r.x = pack_bf16x2(lk.v[i][0] * scale, lk.v[i][1] * scale);
+    r.y = pack_bf16x2(lk.v[i][2] * scale, lk.v[i][3] * scale);
+    r.z = pack_bf16x2(lk.v[i][4] * scale, lk.v[i][5] * scale);
+    r.w = pack_bf16x2(lk.v[i][6] * scale, lk.v[i][7] * scale);
+    if (i == 0) ldsw128<0>(dst, r);
+    if (i == 1) ldsw128<64 * 128>(dst, r);
+    if (i == 2) ldsw128<128 * 128>(dst, r);
+  }
+}
+static_assert(kDw == 3, "decode_store writes three rows");
+
+// Copies of x k-step kt into a ring stage: position P (16-byte unit) of the
+// 32 KiB stage -> row P / 8, slot P % 8 holding unit (P % 8) ^ (row & 7).
+// Rows past M are clamped (their results are never stored).
+__device__ __forceinline__ void issue_x(const PrefillParams& p, char* stage, int m0, int kt, int wave, int lane) {
+#pragma unroll
+  for (int d = 0; d < kXCopies; ++d) {
+    const int pos = (wave * kXCopies + d) * 64 + lane;
+    const int row = pos >> 3;
+    const int u = (pos & 7) ^ (row & 7);
+    const int tok = min(m0 + row, p.m - 1);
+    copy16(p.x + int64_t(tok) * p.x_stride + kt * kBK + u * 8, stage + (wave * kXCopies + d) * 1024);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));  // lgkmcnt(N) only
+}
+
+template <bool kLora>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) char xring[kXD * kXBytes];
+  __shared__ __attribute__((aligned(16))) uint4 wdec[2][kBN * 8];
+  __shared__ __attribute__((aligned(256))) float table[16];
   const int tid = threadIdx.x;
-  if (tid < 16) table[tid] = p.code[tid];
-  if constexpr (kDouble) code2[tid] = p.src.code2[tid];
   const int mt = blockIdx.x % p.mtiles;
   const int nt = blockIdx.x / p.mtiles;
   const int m0 = mt * kBM;
   const int n0 = nt * kBN;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int wm = wave & 1;
   const int wn = wave >> 1;
-  const int lr = lane & 15;
-  const int gq = lane >> 4;
-  __syncthreads();
-  const float offset = kDouble ? *p.src.offset : 0.f;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int nk = p.k / kBK;
 
-  // Global load assignment.
-  const int xrow = tid >> 3;   // + 32 * i
-  const int xunit = tid & 7;
-  const int wrow = tid >> 1;
-  const int whalf = tid & 1;
-  const bool wvalid = n0 + wrow < p.n;
-  const uint8_t* wsrc = p.q + (int64_t(n0 + wrow) * p.k) / 2 + whalf * 16;
-  const int64_t sblock0 = (int64_t(n0 + wrow) * p.k) / kNf4Block;
-
-  uint4 xr[8];
-  uint4 wr;
-  float wscale;
-  auto load_tile = [&](int kt) {
+  WLane wl;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = m0 + xrow + 32 * i;
-      xr[i] = row < p.m ? *reinterpret_cast<const uint4*>(p.x + int64_t(row) * p.x_stride + kt * kBK + xunit * 8)
-                        : make_uint4(0, 0, 0, 0);
-    }
-    if (wvalid) {
-      wr = *reinterpret_cast<const uint4*>(wsrc + kt * (kBK / 2));
-      wscale = block_scale(p.src, sblock0 + kt, code2, offset);
-    } else {
-      wr = make_uint4(0, 0, 0, 0);
-      wscale = 0.f;
-    }
-  };
+  for (int i = 0; i < kDw; ++i) {
+    const int nrow = min(n0 + (tid >> 3) + 64 * i, p.n - 1);
+    wl.qoff[i] = uint32_t(int64_t(nrow) * (p.k >> 1) + (tid & 7) * 4);
+    wl.soff[i] = uint32_t(int64_t(nrow) * (p.k / kNf4Block) * 4);
+  }
 
-  f32x4 acc[8][4];
+  // Prologue in the loop's request order: W(0), x(0), W(1), x(1) (a single
+  // step requests step 0 twice).
+  Packed wa, wb;
+  issue_w(p, 0, wl, wb);
+  issue_x(p, xring, m0, 0, wave, lane);
+  issue_w(p, min(1, nk - 1), wl, wa);
+  issue_x(p, xring + kXBytes, m0, min(1, nk - 1), wave, lane);
+  if (tid < 16) table[tid] = sload(p.code, tid);
+  __syncthreads();  // codebook staged
+  const uint32_t table_addr = lds_addr(table);
+  // Decoded-W store address of this lane (slot 0): row tid >> 3, unit tid & 7.
+  const uint32_t wdst = lds_addr(wdec) + uint32_t((tid >> 3) * 128 + (((tid & 7) ^ ((tid >> 3) & 7)) << 4));
+  constexpr int kW = Packed::kLoads;
+  wait_vm<kW + 2 * kXCopies>();
+  tie_w(wb);
+  {
+    LookAddr la;
+    Looked lk;
+    lookup_addresses(wb, table_addr, la);
+#pragma unroll
+    for (int i = 0; i < kDw; ++i) lookup_dword(la, i, lk);
+    wait_lgkm<0>();
+    tie_lookups(lk);
+    decode_store(wb, lk, wdst);
+  }
+  wait_vm<kW + kXCopies>();
+  lds_barrier();
+
+  f32x4 acc[8][kJ];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kJ; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  const int nk = p.k / kBK;
-  load_tile(0);
-  for (int kt = 0; kt < nk; ++kt) {
+  // Fragment addresses (stage 0) for k halves 0 and 1. Rows of a lane differ
+  // by multiples of 16, so its fragments share the swizzle (row & 7) = (c & 7)
+  // and differ by immediate offsets.
+  const uint32_t xa0 = lds_addr(xring) + uint32_t((wm * 128 + c) * 128 + ((g ^ (c & 7)) << 4));
+  const uint32_t xa1 = lds_addr(xring) + uint32_t((wm * 128 + c) * 128 + (((4 + g) ^ (c & 7)) << 4));
+  const uint32_t wa0 = lds_addr(wdec) + uint32_t((wn * 48 + c) * 128 + ((g ^ (c & 7)) << 4));
+  const uint32_t wa1 = lds_addr(wdec) + uint32_t((wn * 48 + c) * 128 + (((4 + g) ^ (c & 7)) << 4));
+
+  // Fragment reads: k half h of stage kt (x ring slot kt % 3, decoded-W
+  // slot kt & 1); 8 A and kJ B reads of 16 bytes, untracked.
+  auto read_half = [&](int kt, int h, u32x4 (&a)[8], u32x4 (&b)[kJ]) {
+    const uint32_t ax = (h ? xa1 : xa0) + uint32_t((kt % kXD) * kXBytes);
+    const uint32_t bx = (h ? wa1 : wa0) + uint32_t((kt & 1) * kWBytes);
+    a[0] = ldsr128<0 * 2048>(ax);
+    a[1] = ldsr128<1 * 2048>(ax);
+    a[2] = ldsr128<2 * 2048>(ax);
+    a[3] = ldsr128<3 * 2048>(ax);
+    a[4] = ldsr128<4 * 2048>(ax);
+    a[5] = ldsr128<5 * 2048>(ax);
+    a[6] = ldsr128<6 * 2048>(ax);
+    a[7] = ldsr128<7 * 2048>(ax);
+    b[0] = ldsr128<0 * 2048>(bx);
+    b[1] = ldsr128<1 * 2048>(bx);
+    b[2] = ldsr128<2 * 2048>(bx);
+  };
+  constexpr int kHalfReads = 8 + kJ;
+
+  // One k-step, entered with the k-half-0 fragments of stage kt requested:
+  // request step kt + 2 (W into `ld`; past the end the last step again, into
+  // buffers nothing reads), decode W(kt + 1) from `dec` into the other
+  // decoded-W slot over the k-half-0 MFMAs, meet the other waves once x(kt + 1)
+  // landed, then request the next step's k-half-0 fragments and contract
+  // k half 1.
+  u32x4 a0[8], b0[kJ];
+  read_half(0, 0, a0, b0);
+  auto step = [&](int kt, Packed& dec, Packed& ld) {
+    const int kr = min(kt + 2, nk - 1);
+    issue_w(p, kr, wl, ld);
+    issue_x(p, xring + ((kt + 2) % kXD) * kXBytes, m0, kr, wave, lane);
+    u32x4 a1[8], b1[kJ];
+    read_half(kt, 1, a1, b1);
+    // W(kt + 1) was requested before x(kt + 1) and this step's requests.
+    wait_vm<kW + 2 * kXCopies>();
+    tie_w(dec);
+    LookAddr la;
+    lookup_addresses(dec, table_addr, la);
+    wait_lgkm<kHalfReads>();  // the k-half-0 fragments
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xs[swz(xrow + 32 * i, xunit)] = xr[i];
-    ws[swz(wrow, whalf * 4 + 0)] = decode_dword(wr.x, wscale, table);
-    ws[swz(wrow, whalf * 4 + 1)] = decode_dword(wr.y, wscale, table);
-    ws[swz(wrow, whalf * 4 + 2)] = decode_dword(wr.z, wscale, table);
-    ws[swz(wrow, whalf * 4 + 3)] = decode_dword(wr.w, wscale, table);
-    __syncthreads();
-    if (kt + 1 < nk) load_tile(kt + 1);
+    for (int i = 0; i < 8; ++i) tie(a0[i]);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 af[8], bf[4];
+    for (int j = 0; j < kJ; ++j) tie(b0[j]);
+    __builtin_amdgcn_sched_barrier(0);
+    // The lookups between the first k-half-0 MFMAs.
+    Looked lk;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) af[i] = as_bf16x8(xs[swz(wm * 128 + i * 16 + lr, ks * 4 + gq)]);
+    for (int i = 0; i < kDw; ++i) {
+      lookup_dword(la, i, lk);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = as_bf16x8(ws[swz(wn * 64 + j * 16 + lr, ks * 4 + gq)]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a0[i]), vec_bf16x8(b0[j]), acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
-  }
-
-  // ---- epilogue ----------------------------------------------------------
-  // acc[i][j][e] = C[token m0 + wm*128 + 16i + 4gq + e][feature n0 + wn*64 + 16j + lr]
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 64 + j * 16 + lr;
+    for (int j = 0; j < kJ; ++j) acc[kDw][j] = mfma16(vec_bf16x8(a0[kDw]), vec_bf16x8(b0[j]), acc[kDw][j]);
+    __builtin_amdgcn_sched_barrier(0);
+    // Scaling, rounding and stores of W(kt + 1) over the remaining MFMAs.
+    wait_lgkm<0>();  // the lookups (and the k-half-1 fragments before them)
+    tie_lookups(lk);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tie(a1[i]);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) tie(b1[j]);
+#pragma unroll
+    for (int i = kDw + 1; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a0[i]), vec_bf16x8(b0[j]), acc[i][j]);
+    decode_store(dec, lk, wdst + uint32_t(((kt + 1) & 1) * kWBytes));
+#pragma unroll
+    for (int q = 0; q < (8 - kDw - 1) * kJ; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // x(kt + 1) has landed once at most this step's requests are outstanding;
+    // the barrier publishes it with the decoded W(kt + 1), and frees the
+    // slots read at kt - 1 for the requests of step kt + 1.
+    wait_vm<kW + kXCopies>();
+    lds_barrier();
+    read_half(kt + 1, 0, a0, b0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a1[i]), vec_bf16x8(b1[j]), acc[i][j]);
+  };
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, wa, wb);
+    if (kt + 1 < nk) step(kt + 1, wb, wa);
+  }
+  wait_lgkm<0>();  // the fragment reads past the end
+  wait_vm<0>();  // the requests past the end
+
+  // ---- epilogue: acc[i][j][e] = C[token m0 + wm*128 + 16i + 4g + e][feature n0 + wn*48 + 16j + c]
+  const int wn0 = n0 + wn * 48;
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const int n = wn0 + j * 16 + c;
     const float bias = (p.bias && n < p.n) ? bf16_to_f32(p.bias[n]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -271,84 +506,84 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(PrefillParams
       }
   }
   if constexpr (kLora) {
+    // Slot lists and per-slot metadata in the (idle) decoded-W buffer, the
+    // z rows in the (idle) x ring.
+    int* tslot = reinterpret_cast<int*>(&wdec[0][0]);
+    int* list = tslot + kBM;
+    int* mrank = list + kMaxList + 1;
+    int* mstride = mrank + kMaxList;
+    float* mscale = reinterpret_cast<float*>(mstride + kMaxList);
+    int64_t* mboff = reinterpret_cast<int64_t*>(&wdec[1][0]);
+    static_assert(sizeof(wdec[0]) >= (kBM + 4 * kMaxList + 1) * 4 && sizeof(wdec[1]) >= kMaxList * 8,
+                  "slot metadata fits the decoded-W buffer");
+    uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle
     live_slots(p, m0, min(kBM, p.m - m0), tslot, list);
     const int nd = list[kMaxList];
     const int zw = p.slices * kZSlice;
-    const int wn0 = n0 + wn * 64;
-    // Per distinct slot metadata in the (idle) W buffer.
-    int* mrank = reinterpret_cast<int*>(ws);
-    int* mstride = mrank + kMaxList;
-    float* mscale = reinterpret_cast<float*>(mstride + kMaxList);
-    int64_t* mboff = reinterpret_cast<int64_t*>(mscale + kMaxList);
-    static_assert(sizeof(ws) >= kMaxList * (3 * 4 + 8), "slot metadata fits the W buffer");
     for (int d = tid; d < nd; d += kThreads) {
-      const int g = list[d];
-      mrank[d] = p.ranks[g];
-      mstride[d] = p.b_strides[g];
-      mscale[d] = p.lscales[g];
-      mboff[d] = p.b_offsets[g];
+      const int gg = list[d];
+      mrank[d] = p.ranks[gg];
+      mstride[d] = p.b_strides[gg];
+      mscale[d] = p.lscales[gg];
+      mboff[d] = p.b_offsets[gg];
     }
     for (int s = 0; s < p.slices; ++s) {
       const int lo = p.slice_offsets[s];
       const int hi = p.slice_offsets[s + 1];
-      // Every token's z row of this slice (zeros past its rank; zeros for
-      // base-only tokens) is staged once in the x buffer, [token][64] bf16
-      // with the x swizzle; each slot's pass reads the rows it needs.
-      __syncthreads();  // previous users of xs (and the metadata stores) are done
+      __syncthreads();  // previous readers of zs (and the metadata stores) are done
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int row = (tid >> 3) + 32 * q;
+      for (int q = 0; q < kBM * 8 / kThreads; ++q) {
+        const int row = (tid >> 3) + (kThreads / 8) * q;
         const int unit = tid & 7;
         uint4 v = make_uint4(0, 0, 0, 0);
         if (tslot[row] >= 0) v = *reinterpret_cast<const uint4*>(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + unit * 8);
-        xs[swz(row, unit)] = v;
+        zs[swz(row, unit)] = v;
       }
       __syncthreads();
-      if (hi <= wn0 || lo >= wn0 + 64) continue;  // this wave's 64 columns miss the slice
+      if (hi <= wn0 || lo >= wn0 + 48) continue;  // this wave's 48 columns miss the slice
       for (int d = 0; d < nd; ++d) {
-        const int g = list[d];
-        // Bit 4i + e: the lane's row wm*128 + 16i + 4gq + e is routed to g.
+        const int gd = list[d];
+        // Bit 4i + e: the lane's row wm*128 + 16i + 4g + e is routed to gd.
         uint32_t mine = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int4 ts = *reinterpret_cast<const int4*>(tslot + wm * 128 + i * 16 + 4 * gq);
-          mine |= (uint32_t(ts.x == g) | uint32_t(ts.y == g) << 1 | uint32_t(ts.z == g) << 2 | uint32_t(ts.w == g) << 3)
+          const int4 ts = *reinterpret_cast<const int4*>(tslot + wm * 128 + i * 16 + 4 * g);
+          mine |= (uint32_t(ts.x == gd) | uint32_t(ts.y == gd) << 1 | uint32_t(ts.z == gd) << 2 |
+                   uint32_t(ts.w == gd) << 3)
                   << (4 * i);
         }
-        if (__ballot(mine != 0) == 0) continue;  // none of this wave's 128 rows takes g
-        // B fragments of slot d: 4 column blocks, up to 2 k-steps (r <= 64).
+        if (__ballot(mine != 0) == 0) continue;  // none of this wave's 128 rows takes gd
         const int r = mrank[d];
         const int br = mstride[d];
         const uint16_t* bg = p.b_store + mboff[d];
-        bf16x8 b0[4], b1[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = wn0 + j * 16 + lr;
-          uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-          if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, gq * 8, br);
-          if (r > 32 && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + gq * 8, br);
-          b0[j] = as_bf16x8(v0);
-          b1[j] = as_bf16x8(v1);
-        }
         const bool two = r > 32;
         const float scale = mscale[d];
+        bf16x8 lb0[kJ], lb1[kJ];
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+          const int n = wn0 + j * 16 + c;
+          uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+          if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, g * 8, br);
+          if (two && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + g * 8, br);
+          lb0[j] = as_bf16x8(v0);
+          lb1[j] = as_bf16x8(v1);
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          if (__ballot((mine >> (4 * i)) & 15u) == 0) continue;  // no row of this 16-row block takes g
-          const int arow = wm * 128 + i * 16 + lr;
-          const bf16x8 z0 = as_bf16x8(xs[swz(arow, gq)]);
-          const bf16x8 z1 = as_bf16x8(xs[swz(arow, 4 + gq)]);
+          if (__ballot((mine >> (4 * i)) & 15u) == 0) continue;  // no row of this 16-row block takes gd
+          const int arow = wm * 128 + i * 16 + c;
+          const bf16x8 z0 = as_bf16x8(zs[swz(arow, g)]);
+          const bf16x8 z1 = as_bf16x8(zs[swz(arow, 4 + g)]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < kJ; ++j) {
             f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
-            dacc = mfma16(z0, b0[j], dacc);
-            if (two) dacc = mfma16(z1, b1[j], dacc);
-            const int n = wn0 + j * 16 + lr;
+            dacc = mfma16(z0, lb0[j], dacc);
+            if (two) dacc = mfma16(z1, lb1[j], dacc);
+            const int n = wn0 + j * 16 + c;
             const bool col = n >= lo && n < hi;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int e = 0; e < 4; ++e)
               if (col && ((mine >> (4 * i + e)) & 1u)) acc[i][j][e] = round_bf16(acc[i][j][e] + round_bf16(dacc[e] * scale));
-            }
           }
         }
       }
@@ -358,35 +593,57 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_gemm_kernel(PrefillParams
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int m = m0 + wm * 128 + i * 16 + 4 * gq + e;
+      const int m = m0 + wm * 128 + i * 16 + 4 * g + e;
       if (m >= p.m) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 64 + j * 16 + lr;
+      for (int j = 0; j < kJ; ++j) {
+        const int n = wn0 + j * 16 + c;
         if (n < p.n) p.y[int64_t(m) * p.y_stride + n] = uint16_t(f32_to_bf16(acc[i][j][e]));
       }
     }
 }
 
+}  // namespace wide
+
 }  // namespace
 
-int64_t prefill_workspace_bytes(int64_t m, int64_t, int64_t, int slices, int) {
-  return kWorkspaceHeader + (m * slices * kZSlice * 2 + 255) / 256 * 256 + 256;
+namespace {
+int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
+}  // namespace
+
+// Workspace: the decode control header, the z rows (m x slices x 64 bf16),
+// then room for the fp32 block scales of a double-quant weight.
+int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int) {
+  return kWorkspaceHeader + align256(m * slices * kZSlice * 2) + align256(n * (k / kNf4Block) * 4) + 256;
 }
 
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                             void* workspace, int64_t workspace_bytes, void* stream) {
   const int slices = lora ? lora->num_slices : 1;
+  const bool dq = w->scales == nullptr;
   const int64_t need = prefill_workspace_bytes(m, w->n, w->k, slices, lora ? lora->max_rank : 1);
-  LF_REQUIRE(!lora || (workspace && workspace_bytes >= need && aligned16(workspace)),
+  LF_REQUIRE(!(lora || dq) || (workspace && workspace_bytes >= need && aligned16(workspace)),
              "workspace too small: need %lld bytes", (long long)need);
+  auto s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const float* scales = w->scales;
+  if (dq) {
+    // The GEMM streams fp32 block scales: rebuild them from the nested state
+    // (the same reconstruction as the dequantisation kernel) after the z rows.
+    const int64_t nblocks = w->n * (w->k / kNf4Block);
+    float* rebuilt = reinterpret_cast<float*>(ws + kWorkspaceHeader + align256(m * slices * kZSlice * 2));
+    const int rc = lf_nf4_prepare_scales_dq(w->absmax_q, w->absmax2, w->code2, w->offset, w->dq_block, rebuilt,
+                                            nblocks, stream);
+    if (rc != kOk) return rc;
+    scales = rebuilt;
+  }
   PrefillParams p{};
   p.x = x;
   p.x_stride = x_stride;
   p.m = int(m);
   p.q = w->qweight;
-  p.src = ScaleSource{w->scales, w->absmax_q, w->absmax2, w->code2, w->offset, int(w->dq_block)};
+  p.src = ScaleSource{scales, nullptr, nullptr, nullptr, nullptr, 1};
   p.code = w->code;
   p.n = int(w->n);
   p.k = int(w->k);
@@ -394,10 +651,6 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   p.y = y;
   p.y_stride = y_stride;
   p.slices = slices;
-  p.mtiles = int((m + kBM - 1) / kBM);
-  const int ntiles = int((w->n + kBN - 1) / kBN);
-  auto s = static_cast<hipStream_t>(stream);
-  const bool dq = w->scales == nullptr;
   if (lora) {
     p.a_store = lora->a_store;
     p.a_offsets = lora->a_offsets;
@@ -408,18 +661,14 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.lscales = lora->scales;
     p.token_slots = lora->token_slots;
     p.slice_offsets = lora->slice_offsets;
-    p.zpad = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + kWorkspaceHeader);  // after the decode header
+    p.zpad = reinterpret_cast<uint16_t*>(ws + kWorkspaceHeader);  // after the decode header
     hipLaunchKernelGGL(prefill_shrink_kernel, dim3(unsigned((m + 15) / 16)), dim3(kThreads), 0, s, p);
     LF_HIP(hipGetLastError());
   }
-  const dim3 grid(unsigned(p.mtiles * ntiles));
-  if (dq) {
-    if (lora) hipLaunchKernelGGL((prefill_gemm_kernel<true, true>), grid, dim3(kThreads), 0, s, p);
-    else hipLaunchKernelGGL((prefill_gemm_kernel<true, false>), grid, dim3(kThreads), 0, s, p);
-  } else {
-    if (lora) hipLaunchKernelGGL((prefill_gemm_kernel<false, true>), grid, dim3(kThreads), 0, s, p);
-    else hipLaunchKernelGGL((prefill_gemm_kernel<false, false>), grid, dim3(kThreads), 0, s, p);
-  }
+  p.mtiles = int((m + wide::kBM - 1) / wide::kBM);
+  const dim3 grid(unsigned(p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN)));
+  if (lora) hipLaunchKernelGGL((wide::gemm_kernel<true>), grid, dim3(wide::kThreads), 0, s, p);
+  else hipLaunchKernelGGL((wide::gemm_kernel<false>), grid, dim3(wide::kThreads), 0, s, p);
   LF_HIP(hipGetLastError());
   return kOk;
 }

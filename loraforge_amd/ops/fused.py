@@ -111,14 +111,17 @@ def _workspace(device, stream: int, size: int):
         return ws
 
 
-def _decode_takes_nested(m: int, n: int, k: int, dq_block: int) -> bool:
-    """Whether the kernel for ``m`` tokens rebuilds double-quant scales itself.
+def _kernel_takes_nested(m: int, exact: bool) -> bool:
+    """Whether the call for ``m`` tokens passes a nested state to the library.
 
-    The prefill GEMM (m > 64) decodes the nested state per tile; the decode
-    kernel streams fp32 block scales, so decode calls take the prepared
-    scales, rebuilt once per weight and cached on the state.
+    The decode kernel streams fp32 block scales, so decode calls take the
+    prepared scales, rebuilt once per weight and cached on the state. The
+    prefill launch rebuilds them itself into its workspace on every call;
+    by default prefill calls also take the cached scales (no per-call
+    rebuild), and ``exact=True`` passes the nested state (the results are
+    identical).
     """
-    return m > 64
+    return m > 64 and exact
 
 
 def _prepared_scales(state):
@@ -136,7 +139,7 @@ def _prepared_scales(state):
     return cached
 
 
-def _weight_struct(qweight, state, scales, n, k, device, m=0):
+def _weight_struct(qweight, state, scales, n, k, device, m=0, exact=False):
     import torch
 
     code = state.code
@@ -150,7 +153,7 @@ def _weight_struct(qweight, state, scales, n, k, device, m=0):
     keep = [qweight, code]
     if scales is None and not state.nested:
         scales = state.absmax
-    if scales is None and not _decode_takes_nested(m, n, k, int(state.state2.blocksize)):
+    if scales is None and not _kernel_takes_nested(m, exact):
         scales = _prepared_scales(state)
     if scales is not None:
         vector(scales.reshape(-1), "scales", torch.float32, device, n * k // 64)
@@ -231,11 +234,11 @@ def nf4_lora_linear(
     Launches on the current stream; the workspace (cached per device and
     stream unless passed) must not be shared by overlapping calls.
 
-    Decode batches (<= 64 tokens) contract ``bf16(code[nibble])`` on MFMA and
-    apply each fp32 block scale to the block's partial sum; ``exact=True``
-    instead multiplies the reference's dequantised weights
-    ``bf16_rne(code * scale)`` (bit-identical W, slower). Prefill always uses
-    the exact weights.
+    The prefill GEMM (more than 64 tokens) always multiplies the reference's
+    dequantised weights ``bf16_rne(code * scale)``. By default the decode
+    kernel (<= 64 tokens) contracts ``bf16(code[nibble])`` on MFMA and applies
+    each fp32 block scale to the block's partial sum; ``exact=True`` makes it
+    multiply the exact weights too (bit-identical W, slower).
     """
     import torch
 
@@ -273,7 +276,7 @@ def nf4_lora_linear(
     if m == 0:
         return out
     require_arch(device)
-    w, keep = _weight_struct(qweight, state, scales, n, k, device, m)
+    w, keep = _weight_struct(qweight, state, scales, n, k, device, m, exact)
     lib = _lib.library()
     slices = lora.num_slices if lora is not None else 1
     max_rank = lora.max_rank if lora is not None else 1

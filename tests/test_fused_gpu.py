@@ -185,6 +185,31 @@ def test_prefill_segments(m, dq, device):
     close(bits(y), _cases.fused_expected(case))
 
 
+@pytest.mark.parametrize("k", [64, 192, 320])
+@pytest.mark.parametrize("dq", [False, True])
+def test_prefill_short_and_odd_k(k, dq, device):
+    """One, three and five k-steps (the pipeline's requests past the end), ragged N and M."""
+    m = 300
+    slots = np.repeat(np.array([0, 1, -1], np.int32), [100, 150, 50])
+    case = _cases.fused_case(m, 320, k, ranks=(8, 32), double_quant=dq, seed=k + dq, token_slots=slots)
+    x, q, st, lora, _ = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, lora=lora)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+
+
+@pytest.mark.parametrize("dq", [False, True])
+def test_prefill_exact_weights(dq, device):
+    """exact=True hands the nested state to the launch, which rebuilds the fp32 scales in its workspace."""
+    m = 200
+    slots = np.repeat(np.array([1, -1, 0], np.int32), [90, 30, 80])
+    case = _cases.fused_case(m, 384, 512, ranks=(16, 8), double_quant=dq, seed=77, token_slots=slots, bias=True)
+    x, q, st, lora, bias = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora, exact=True)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+
+
 def test_prefill_slices_and_interleaved_routes(device):
     ranks = (8, 64, 0, 17)
     case = _cases.fused_case(300, 512, 256, ranks=ranks, slices=3, bounds=[0, 200, 448, 512], seed=5, null_frac=0.1)
