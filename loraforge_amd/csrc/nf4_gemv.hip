@@ -19,6 +19,7 @@
 // read from HBM once).
 #include <algorithm>
 
+#include "call_epoch.h"
 #include "lds_pipeline.h"
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
@@ -80,9 +81,7 @@ struct GemvParams {
   int kz_len;     // k per slice (multiple of 64)
   int producers;  // workgroups b < producers make units b, b + producers, ...
   int* status;    // set to 1 when a bounded wait times out
-  uint32_t* epoch;   // the call's tag is epoch + 1
-  uint32_t* groups;  // [8] arrival counts, 128 bytes apart (workgroup b counts in b % 8)
-  uint32_t* total;   // groups complete in this call
+  CallEpoch ce;      // call tag: epoch + 1, moved on by the last workgroup
   uint64_t* zp;      // [units][zw] shrink partial sums as (tag << 32) | fp32 bits
 };
 
@@ -219,15 +218,9 @@ __device__ __forceinline__ void contract(const Frags<TL>& f, int kb, int kend, f
 // with the call's tag. The fragments of a workgroup's first unit are
 // requested between its first and second weight stages, so they are not
 // queued behind the whole prologue.
-// Call tag: every workgroup reads the epoch word at its start; the call's
-// tag is epoch + 1. When its work is done, the LoRA wave counts the
-// workgroup in (one counter per blockIdx % 8, so no single address takes
-// every atomic); the last of a group counts the group in, and the last group
-// resets the counters and moves the epoch on. Every workgroup has read the
-// epoch before it counts in, so all workgroups of a call see the same tag
-// and no earlier call used it (tags cycle through 1 .. 2^32 - 1; zero never
-// marks data, so a zeroed workspace holds no valid entry). An entry is valid
-// for a call iff its tag is the call's: nothing is reset between calls.
+// Call tag (call_epoch.h): every workgroup reads the epoch at its start and
+// the LoRA wave counts the workgroup in when its work is done. An entry is
+// valid for a call iff its tag is the call's: nothing is reset between calls.
 // Expand: the LoRA wave of every workgroup lists its tile's tokens and
 // distinct slots, then polls the partials of its routed tokens until all
 // carry the call's tag and sums their k-slices into z = bf16(sum) in LDS.
@@ -246,38 +239,6 @@ __device__ __forceinline__ void tagged_store(uint64_t* p, float v, uint32_t tag)
 }
 __device__ __forceinline__ uint64_t tagged_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// A per-lane zero the compiler cannot see through: an atomic on a provably
-// uniform address is turned into a wave-wide one whose result is waited for
-// on the spot.
-__device__ __forceinline__ uint32_t opaque_zero() {
-  uint32_t z;
-  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
-  return z;
-}
-
-// Counts this workgroup in (lane 0); the old count is returned in lane 0 and
-// nothing waits for it until depart_finish.
-__device__ __forceinline__ uint32_t depart_issue(const GemvParams& p, int lane) {
-  uint32_t* counter = p.groups + 32 * (blockIdx.x & 7) + opaque_zero();
-  uint32_t old = 0;
-  if (lane == 0) old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return old;
-}
-
-// The last workgroup of its group counts the group in; the last group
-// resets the counts and moves the epoch on.
-__device__ __forceinline__ void depart_finish(const GemvParams& p, uint32_t old, uint32_t epoch, int lane) {
-  if (lane != 0) return;
-  const uint32_t g = blockIdx.x & 7;
-  const uint32_t members = (gridDim.x - g + 7) / 8;
-  if (old != members - 1) return;
-  __hip_atomic_store(p.groups + 32 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t groups = gridDim.x < 8 ? gridDim.x : 8u;
-  if (__hip_atomic_fetch_add(p.total, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != groups - 1) return;
-  __hip_atomic_store(p.total, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(p.epoch, epoch + 1 == 0xffffffffu ? 0u : epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct Unit {
@@ -927,7 +888,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     for (int s = 1; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
   } else if constexpr (kLora) {
     // The LoRA wave: the epoch and its tile's token metadata.
-    epoch = __hip_atomic_load(p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     tmeta = token_meta(p, t0, mt, lane);
     has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
   }
@@ -1029,7 +990,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     f32x4 dacc[RT][TT];
     if (wave == kBase) {
       lora_gather<TL>(p, lora7, t0, mt, __builtin_amdgcn_readfirstlane(epoch) + 1u, lane);
-      departed = depart_issue(p, lane);  // after the last partial load: nothing waits for it until the end
+      departed = depart_issue(p.ce, lane);  // after the last partial load: nothing waits for it until the end
     } else {
       if (has0 && nst < 2) {
         wait_vm<0>();
@@ -1095,7 +1056,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       }
     }
   }
-  if (kLora && wave == kBase) depart_finish(p, departed, __builtin_amdgcn_readfirstlane(epoch), lane);
+  if (kLora && wave == kBase) depart_finish(p.ce, departed, __builtin_amdgcn_readfirstlane(epoch), lane);
 }
 
 template <int RT, int XR, bool kLora>
@@ -1136,13 +1097,9 @@ struct GemvPlan {
 // Shrink units: m tokens x kz k-slices, kz chosen so that m * kz is about
 // min(grid, CUs) (one unit per producing workgroup when m allows) and a
 // consumer's partial reads fit one batch.
-// Control header layout: epoch, status, eight group arrival counts (128
-// bytes apart), the group total, then the tagged shrink partials (at most
-// 64 tokens x 192 values x 8 bytes).
-constexpr int64_t kEpochOffset = 0;
-constexpr int64_t kStatusOffset = 8;
-constexpr int64_t kGroupsOffset = 128;
-constexpr int64_t kTotalOffset = kGroupsOffset + 8 * 128;
+// Control header layout: the call-epoch words and the status word
+// (call_epoch.h), then the tagged shrink partials (at most 64 tokens x 192
+// values x 8 bytes).
 constexpr int64_t kPartialsOffset = 2048;
 
 GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
@@ -1216,10 +1173,8 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
     p.kz_len = pl.kz_len;
     p.producers = pl.producers;
     char* ws = static_cast<char*>(workspace);
-    p.epoch = reinterpret_cast<uint32_t*>(ws + kEpochOffset);
+    p.ce = call_epoch_of(ws);
     p.status = reinterpret_cast<int*>(ws + kStatusOffset);
-    p.groups = reinterpret_cast<uint32_t*>(ws + kGroupsOffset);
-    p.total = reinterpret_cast<uint32_t*>(ws + kTotalOffset);
     p.zp = reinterpret_cast<uint64_t*>(ws + kPartialsOffset);
   }
   const dim3 grid(unsigned(pl.grid));

@@ -5,19 +5,24 @@
 // LoRA part):  y = bf16(x @ dequant(W)^T) (+bias);  z = bf16(A_g x);
 //              y = bf16(y + bf16(scale_g * B_g z)).
 //
-// Two launches on the caller's stream:
-//  1. shrink: per 16-token block and distinct slot, z = bf16(x A_g^T) on
-//     MFMA into a slice-padded workspace zpad[m][s*64 + j] (zeros past r).
-//  2. GEMM (wide::gemm_kernel): workgroup tile 256 tokens x 192 output
-//     features; x streamed by direct global -> LDS copies, W decoded once per
-//     tile to the reference's exact weights bf16_rne(code * scale) (fp32 or
-//     double-quant block scales) into LDS, contracted on
-//     v_mfma_f32_16x16x32_bf16. LDS rows are 128 B with a 16-byte-unit XOR
-//     swizzle (unit ^ row % 8). Epilogue: round, bias, then per slice the
-//     tile's z rows are staged in LDS once and, for every distinct slot in
-//     the tile, a second MFMA pass z x B_g^T over the 16-row blocks holding
-//     its tokens gives the LoRA delta, applied with the reference's two bf16
-//     roundings to the rows routed to that slot.
+// One launch (wide::gemm_kernel) on the caller's stream (a double-quant
+// weight first gets its fp32 block scales rebuilt into the workspace):
+//  - LoRA launches start with one z producer per 256-token tile: z =
+//    bf16(x A_g^T) of the tile's routed tokens, on the GEMM's own LDS
+//    pipeline and MFMA fragments, into a slice-padded workspace
+//    zpad[m][s*64 + j] (zeros past r), then the tile's flag is set to the
+//    call's tag (call_epoch.h).
+//  - GEMM tiles of 256 tokens x 192 output features: x streamed by direct
+//    global -> LDS copies, W decoded once per tile to the reference's exact
+//    weights bf16_rne(code * scale) into LDS, contracted on
+//    v_mfma_f32_16x16x32_bf16. LDS rows are 128 B with a 16-byte-unit XOR
+//    swizzle (unit ^ row % 8). Epilogue: round, bias; with LoRA, wait for the
+//    tile's flag (its producer has a lower block id, so it is already
+//    running), stage the tile's z rows per slice in LDS and, for every
+//    distinct slot in the tile, a second MFMA pass z x B_g^T over the 16-row
+//    blocks holding its tokens gives the delta, applied with the reference's
+//    two bf16 roundings to the rows routed to that slot.
+#include "call_epoch.h"
 #include "lds_pipeline.h"
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
@@ -52,7 +57,9 @@ struct PrefillParams {
   const int32_t* token_slots;
   const int32_t* slice_offsets;
   int slices;
-  uint16_t* zpad;  // [m][slices * 64]
+  uint16_t* zpad;     // [m][slices * 64]
+  uint32_t* zflags;   // [mtiles]: the call's tag once the tile's z rows are stored
+  CallEpoch ce;
   int mtiles;
 };
 
@@ -92,69 +99,6 @@ __device__ void live_slots(const PrefillParams& p, int t0, int count, int* tslot
     if (lane == 0) list[kMaxList] = nd;
   }
   __syncthreads();
-}
-
-// ---------------------------------------------------------------------------
-// 1. shrink into zpad.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void prefill_shrink_kernel(PrefillParams p) {
-  __shared__ int list[kMaxList + 1];
-  __shared__ int tslot[kThreads];
-  __shared__ int trank[16];
-  const int t0 = blockIdx.x * 16;
-  const int count = min(16, p.m - t0);
-  live_slots(p, t0, count, tslot, list);
-  if (threadIdx.x < 16) trank[threadIdx.x] = tslot[threadIdx.x] >= 0 ? p.ranks[tslot[threadIdx.x]] : 0;
-  __syncthreads();
-  const int nd = list[kMaxList];
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int gq = lane >> 4;
-  const int zw = p.slices * kZSlice;
-  // Zero the padding columns [r, 64) of every live token's slices.
-  for (int i = threadIdx.x; i < count * zw; i += kThreads) {
-    const int t = i / zw;
-    const int col = i - t * zw;
-    const int r = trank[t];
-    if (r > 0 && (col % kZSlice) >= r) p.zpad[int64_t(t0 + t) * zw + col] = 0;
-  }
-  for (int d = 0; d < nd; ++d) {
-    const int g = list[d];
-    const int r = p.ranks[g];
-    const int rows = p.slices * r;
-    const uint16_t* ag = p.a_store + p.a_offsets[g];
-    const int tok = lane & 15;
-    const bool mine = tslot[tok] == g;
-    for (int ct = wave; ct * 16 < rows; ct += 4) {
-      const int j = ct * 16 + (lane & 15);
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      // K is a multiple of 64; 8 steps of 32 k have their loads in flight together.
-      const uint16_t* xrow = p.x + int64_t(t0 + (mine ? tok : 0)) * p.x_stride + gq * 8;
-      const uint16_t* arow = ag + int64_t(j < rows ? j : 0) * p.k + gq * 8;
-      for (int kc = 0; kc < p.k; kc += 8 * 32) {
-        uint4 xv[8], av[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int kk = kc + 32 * i;
-          const bool ok = kk < p.k;
-          xv[i] = ok && mine ? *reinterpret_cast<const uint4*>(xrow + kk) : make_uint4(0, 0, 0, 0);
-          av[i] = ok && j < rows ? *reinterpret_cast<const uint4*>(arow + kk) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc = mfma16(as_bf16x8(xv[i]), as_bf16x8(av[i]), acc);
-      }
-      // acc[e] = z[token 4*gq + e][column j]
-      if (j < rows) {
-        const int s = j / r;
-        const int jj = j - s * r;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = 4 * gq + e;
-          if (t < count && tslot[t] == g) p.zpad[int64_t(t0 + t) * zw + s * kZSlice + jj] = uint16_t(f32_to_bf16(acc[e]));
-        }
-      }
-    }
-  }
 }
 
 // LoRA B row segment [kk, kk + 8) of a row of length br (zeros past br).
@@ -330,14 +274,221 @@ __device__ __forceinline__ void wait_lgkm() {
   __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));  // lgkmcnt(N) only
 }
 
+// z producer of M-tile mt (the launch's workgroups below mtiles): z rows
+// bf16(x A_g^T) of every token of the tile routed to a live slot, in the
+// slice-padded layout zpad[t][s * 64 + j] (zeros for j >= r), then the tile's
+// flag is set to the call's tag. The columns of a pass are up to kBN rows of
+// the distinct slots' A factors ([slices * r, K] each, concatenated); a pass
+// streams the x tile and those rows through the GEMM's LDS layout (direct
+// copies, two-step x ring, one-step A slots) and contracts them on the same
+// MFMA fragments; each output is kept for the rows routed to its slot.
+__device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, uint32_t tag, char* xring, uint4* wdec,
+                                          int* tslot, int* list, int* colmap, int* cum) {
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int m0 = mt * kBM;
+  const int count = min(kBM, p.m - m0);
+  const int nk = p.k / kBK;
+  const int zw = p.slices * kZSlice;
+  live_slots(p, m0, count, tslot, list);
+  const int nd = list[kMaxList];
+  // Column offsets of the distinct slots (cum[d] .. cum[d + 1]).
+  if (tid == 0) {
+    int acc = 0;
+    for (int d = 0; d < nd; ++d) {
+      cum[d] = acc;
+      acc += p.slices * p.ranks[list[d]];
+    }
+    cum[nd] = acc;
+  }
+  // Zero columns r .. 64 of every slice of the live tokens.
+  for (int i = tid; i < count * zw; i += kThreads) {
+    const int t = i / zw;
+    const int col = i - t * zw;
+    const int gt = tslot[t];
+    if (gt >= 0 && (col % kZSlice) >= p.ranks[gt]) p.zpad[int64_t(m0 + t) * zw + col] = 0;
+  }
+  __syncthreads();
+  const int ncols = cum[nd];
+  const uint32_t xa0 = lds_addr(xring) + uint32_t((wm * 128 + c) * 128 + ((g ^ (c & 7)) << 4));
+  const uint32_t xa1 = lds_addr(xring) + uint32_t((wm * 128 + c) * 128 + (((4 + g) ^ (c & 7)) << 4));
+  const uint32_t wa0 = lds_addr(wdec) + uint32_t((wn * 48 + c) * 128 + ((g ^ (c & 7)) << 4));
+  const uint32_t wa1 = lds_addr(wdec) + uint32_t((wn * 48 + c) * 128 + (((4 + g) ^ (c & 7)) << 4));
+  for (int c0 = 0; c0 < ncols; c0 += kBN) {
+    // colmap[col] = (distinct slot << 16) | (slice << 8) | row within the slice, or -1.
+    if (tid < kBN) {
+      const int col = c0 + tid;
+      int e = -1;
+      if (col < ncols) {
+        int d = 0;
+        while (cum[d + 1] <= col) ++d;
+        const int rho = col - cum[d];
+        const int r = p.ranks[list[d]];
+        e = (d << 16) | ((rho / r) << 8) | (rho % r);
+      }
+      colmap[tid] = e;
+    }
+    __syncthreads();
+    // This lane's three A-row copies per step: position P = (wave * 3 + q) * 64
+    // + lane -> row P / 8, slot P % 8 holding unit (P % 8) ^ (row & 7).
+    const uint16_t* asrc[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int pos = (wave * 3 + q) * 64 + lane;
+      const int row = pos >> 3;
+      const int u = (pos & 7) ^ (row & 7);
+      const int e = colmap[row];
+      const int d = e < 0 ? 0 : e >> 16;
+      const int rho = e < 0 ? 0 : (((e >> 8) & 0xff) * p.ranks[list[d]] + (e & 0xff));
+      asrc[q] = p.a_store + p.a_offsets[list[d]] + int64_t(rho) * p.k + u * 8;
+    }
+    auto issue_a = [&](int kt, int slot) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        copy16(asrc[q] + kt * kBK, reinterpret_cast<char*>(wdec) + slot * kWBytes + (wave * 3 + q) * 1024);
+    };
+    const bool busy = wn * 48 < ncols - c0;  // the wave's columns hold A rows
+    f32x4 acc[8][kJ];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    issue_x(p, xring, m0, 0, wave, lane);
+    issue_x(p, xring + kXBytes, m0, min(1, nk - 1), wave, lane);
+    issue_a(0, 0);
+    wait_vm<0>();
+    lds_barrier();
+    for (int kt = 0; kt < nk; ++kt) {
+      // Requests: A(kt + 1), then x(kt + 2) (past the end: the last step again).
+      issue_a(min(kt + 1, nk - 1), (kt + 1) & 1);
+      issue_x(p, xring + ((kt + 2) % kXD) * kXBytes, m0, min(kt + 2, nk - 1), wave, lane);
+      if (busy) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t ax = (h ? xa1 : xa0) + uint32_t((kt % kXD) * kXBytes);
+          const uint32_t bx = (h ? wa1 : wa0) + uint32_t((kt & 1) * kWBytes);
+          u32x4 a[8], b[kJ];
+          a[0] = ldsr128<0 * 2048>(ax);
+          a[1] = ldsr128<1 * 2048>(ax);
+          a[2] = ldsr128<2 * 2048>(ax);
+          a[3] = ldsr128<3 * 2048>(ax);
+          a[4] = ldsr128<4 * 2048>(ax);
+          a[5] = ldsr128<5 * 2048>(ax);
+          a[6] = ldsr128<6 * 2048>(ax);
+          a[7] = ldsr128<7 * 2048>(ax);
+          b[0] = ldsr128<0 * 2048>(bx);
+          b[1] = ldsr128<1 * 2048>(bx);
+          b[2] = ldsr128<2 * 2048>(bx);
+          wait_lgkm<0>();
+#pragma unroll
+          for (int i = 0; i < 8; ++i) tie(a[i]);
+#pragma unroll
+          for (int j = 0; j < kJ; ++j) tie(b[j]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a[i]), vec_bf16x8(b[j]), acc[i][j]);
+        }
+      }
+      // A(kt + 1) and x(kt + 1) have landed once at most x(kt + 2) is outstanding.
+      wait_vm<kXCopies>();
+      lds_barrier();
+    }
+    wait_vm<0>();  // the requests past the end
+    // acc[i][j][e] = z[token m0 + wm*128 + 16i + 4g + e][pass column wn*48 + 16j + c]
+    if (busy) {
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int e = colmap[wn * 48 + j * 16 + c];
+        if (e < 0) continue;
+        const int gd = list[e >> 16];
+        const int zc = ((e >> 8) & 0xff) * kZSlice + (e & 0xff);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = wm * 128 + i * 16 + 4 * g + r;
+            if (row < count && tslot[row] == gd)
+              p.zpad[int64_t(m0 + row) * zw + zc] = uint16_t(f32_to_bf16(acc[i][j][r]));
+          }
+      }
+    }
+    __syncthreads();  // colmap and the LDS slots are reused by the next pass
+  }
+  // Publish: every thread's z stores are performed at device scope before the
+  // flag carries the call's tag.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (tid == 0) __hip_atomic_store(p.zflags + mt, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until the z rows of M-tile mt carry the call's tag (their producer
+// has a lower block id, so it has been dispatched before this workgroup).
+// The flag and the z rows are read with device-scope loads (coherent past
+// the caches of this CU and XCD), so no acquire fence is needed: an acquire
+// at device scope would invalidate the whole L2 of the XCD under the other
+// workgroups' feet.
+__device__ __forceinline__ void wait_z(const PrefillParams& p, int mt, uint32_t tag) {
+  if (threadIdx.x == 0) {
+    while (__hip_atomic_load(p.zflags + mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag)
+      __builtin_amdgcn_s_sleep(8);
+  }
+  __syncthreads();
+}
+
+// 16 bytes of z rows read with device-scope loads.
+__device__ __forceinline__ uint4 load_z16(const uint16_t* src) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(src);
+  uint4 v;
+  v.x = __hip_atomic_load(w + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.y = __hip_atomic_load(w + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.z = __hip_atomic_load(w + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.w = __hip_atomic_load(w + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
+}
+
+// Counts the workgroup in; the last one moves the epoch on (call_epoch.h).
+__device__ __forceinline__ void depart(const PrefillParams& p, uint32_t tag) {
+  if (threadIdx.x < 64) {
+    const uint32_t old = depart_issue(p.ce, threadIdx.x);
+    depart_finish(p.ce, old, tag - 1u, threadIdx.x);
+  }
+}
+
+// Block ids below mtiles (LoRA launches only) produce the tiles' z rows;
+// the others are GEMM tiles, M-tile b % mtiles on consecutive ids.
 template <bool kLora>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) char xring[kXD * kXBytes];
   __shared__ __attribute__((aligned(16))) uint4 wdec[2][kBN * 8];
   __shared__ __attribute__((aligned(256))) float table[16];
+  __shared__ __attribute__((aligned(16))) int tslot[kLora ? kBM : 1];
+  __shared__ int list[kLora ? kMaxList + 1 : 1];
+  __shared__ int cum[kLora ? kMaxList + 1 : 1];
+  __shared__ int colmap[kLora ? kBN : 1];
+  __shared__ int mrank[kLora ? kMaxList : 1];
+  __shared__ int mstride[kLora ? kMaxList : 1];
+  __shared__ float mscale[kLora ? kMaxList : 1];
+  __shared__ int64_t mboff[kLora ? kMaxList : 1];
   const int tid = threadIdx.x;
-  const int mt = blockIdx.x % p.mtiles;
-  const int nt = blockIdx.x / p.mtiles;
+  int b = blockIdx.x;
+  uint32_t tag = 0;
+  if constexpr (kLora) {
+    tag = __builtin_amdgcn_readfirstlane(epoch_tag(p.ce));
+    if (b < p.mtiles) {
+      produce_z(p, b, tag, xring, &wdec[0][0], tslot, list, colmap, cum);
+      depart(p, tag);
+      return;
+    }
+    b -= p.mtiles;
+  }
+  const int mt = b % p.mtiles;
+  const int nt = b / p.mtiles;
   const int m0 = mt * kBM;
   const int n0 = nt * kBN;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -383,6 +534,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   }
   wait_vm<kW + kXCopies>();
   lds_barrier();
+  if constexpr (kLora) {
+    // The tile's routes and slot metadata, ahead of the k-loop.
+    live_slots(p, m0, min(kBM, p.m - m0), tslot, list);
+    for (int d = tid; d < list[kMaxList]; d += kThreads) {
+      const int gg = list[d];
+      mrank[d] = p.ranks[gg];
+      mstride[d] = p.b_strides[gg];
+      mscale[d] = p.lscales[gg];
+      mboff[d] = p.b_offsets[gg];
+    }
+  }
 
   f32x4 acc[8][kJ];
 #pragma unroll
@@ -492,6 +654,41 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
 
   // ---- epilogue: acc[i][j][e] = C[token m0 + wm*128 + 16i + 4g + e][feature n0 + wn*48 + 16j + c]
   const int wn0 = n0 + wn * 48;
+  // LoRA: the z rows of slice 0 and the B fragments of the first slot are
+  // requested before the base rounding, so their latency overlaps it.
+  const int nd = kLora ? list[kMaxList] : 0;
+  const int zw = p.slices * kZSlice;
+  constexpr int kZq = kBM * 8 / kThreads;  // 16-byte z units per thread and slice
+  uint4 zr[kZq];
+  bf16x8 lb0[kJ], lb1[kJ];
+  // B fragments of slot d for this wave's columns: k-group g of ranks 0..31 and 32..63.
+  auto load_b = [&](int d) {
+    const int br = mstride[d];
+    const uint16_t* bg = p.b_store + mboff[d];
+    const bool two = mrank[d] > 32;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int n = wn0 + j * 16 + c;
+      uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+      if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, g * 8, br);
+      if (two && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + g * 8, br);
+      lb0[j] = as_bf16x8(v0);
+      lb1[j] = as_bf16x8(v1);
+    }
+  };
+  auto load_zs = [&](int s) {
+#pragma unroll
+    for (int q = 0; q < kZq; ++q) {
+      const int row = (tid >> 3) + (kThreads / 8) * q;
+      zr[q] = make_uint4(0, 0, 0, 0);
+      if (tslot[row] >= 0) zr[q] = load_z16(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + (tid & 7) * 8);
+    }
+  };
+  if constexpr (kLora) {
+    wait_z(p, mt, tag);
+    load_zs(0);
+    if (nd > 0) load_b(0);
+  }
 #pragma unroll
   for (int j = 0; j < kJ; ++j) {
     const int n = wn0 + j * 16 + c;
@@ -506,39 +703,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       }
   }
   if constexpr (kLora) {
-    // Slot lists and per-slot metadata in the (idle) decoded-W buffer, the
-    // z rows in the (idle) x ring.
-    int* tslot = reinterpret_cast<int*>(&wdec[0][0]);
-    int* list = tslot + kBM;
-    int* mrank = list + kMaxList + 1;
-    int* mstride = mrank + kMaxList;
-    float* mscale = reinterpret_cast<float*>(mstride + kMaxList);
-    int64_t* mboff = reinterpret_cast<int64_t*>(&wdec[1][0]);
-    static_assert(sizeof(wdec[0]) >= (kBM + 4 * kMaxList + 1) * 4 && sizeof(wdec[1]) >= kMaxList * 8,
-                  "slot metadata fits the decoded-W buffer");
-    uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle
-    live_slots(p, m0, min(kBM, p.m - m0), tslot, list);
-    const int nd = list[kMaxList];
-    const int zw = p.slices * kZSlice;
-    for (int d = tid; d < nd; d += kThreads) {
-      const int gg = list[d];
-      mrank[d] = p.ranks[gg];
-      mstride[d] = p.b_strides[gg];
-      mscale[d] = p.lscales[gg];
-      mboff[d] = p.b_offsets[gg];
-    }
+    uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle (the ring is idle)
     for (int s = 0; s < p.slices; ++s) {
       const int lo = p.slice_offsets[s];
       const int hi = p.slice_offsets[s + 1];
-      __syncthreads();  // previous readers of zs (and the metadata stores) are done
-#pragma unroll
-      for (int q = 0; q < kBM * 8 / kThreads; ++q) {
-        const int row = (tid >> 3) + (kThreads / 8) * q;
-        const int unit = tid & 7;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (tslot[row] >= 0) v = *reinterpret_cast<const uint4*>(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + unit * 8);
-        zs[swz(row, unit)] = v;
+      if (s > 0) {
+        __syncthreads();  // the previous slice's readers of zs are done
+        load_zs(s);
       }
+#pragma unroll
+      for (int q = 0; q < kZq; ++q) zs[swz((tid >> 3) + (kThreads / 8) * q, tid & 7)] = zr[q];
       __syncthreads();
       if (hi <= wn0 || lo >= wn0 + 48) continue;  // this wave's 48 columns miss the slice
       for (int d = 0; d < nd; ++d) {
@@ -553,21 +727,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
                   << (4 * i);
         }
         if (__ballot(mine != 0) == 0) continue;  // none of this wave's 128 rows takes gd
-        const int r = mrank[d];
-        const int br = mstride[d];
-        const uint16_t* bg = p.b_store + mboff[d];
-        const bool two = r > 32;
+        if (d > 0 || s > 0) load_b(d);
+        const bool two = mrank[d] > 32;
         const float scale = mscale[d];
-        bf16x8 lb0[kJ], lb1[kJ];
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-          const int n = wn0 + j * 16 + c;
-          uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-          if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, g * 8, br);
-          if (two && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + g * 8, br);
-          lb0[j] = as_bf16x8(v0);
-          lb1[j] = as_bf16x8(v1);
-        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           if (__ballot((mine >> (4 * i)) & 15u) == 0) continue;  // no row of this 16-row block takes gd
@@ -601,6 +763,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
         if (n < p.n) p.y[int64_t(m) * p.y_stride + n] = uint16_t(f32_to_bf16(acc[i][j][e]));
       }
     }
+  if constexpr (kLora) depart(p, tag);
 }
 
 }  // namespace wide
@@ -611,10 +774,12 @@ namespace {
 int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 }  // namespace
 
-// Workspace: the decode control header, the z rows (m x slices x 64 bf16),
-// then room for the fp32 block scales of a double-quant weight.
+// Workspace: the control header (call epoch), the z rows (m x slices x 64
+// bf16), room for the fp32 block scales of a double-quant weight, then one
+// z flag per 256-token tile.
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int) {
-  return kWorkspaceHeader + align256(m * slices * kZSlice * 2) + align256(n * (k / kNf4Block) * 4) + 256;
+  return kWorkspaceHeader + align256(m * slices * kZSlice * 2) + align256(n * (k / kNf4Block) * 4) +
+         align256((m + wide::kBM - 1) / wide::kBM * 4) + 256;
 }
 
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
@@ -662,11 +827,13 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.token_slots = lora->token_slots;
     p.slice_offsets = lora->slice_offsets;
     p.zpad = reinterpret_cast<uint16_t*>(ws + kWorkspaceHeader);  // after the decode header
-    hipLaunchKernelGGL(prefill_shrink_kernel, dim3(unsigned((m + 15) / 16)), dim3(kThreads), 0, s, p);
-    LF_HIP(hipGetLastError());
+    p.zflags = reinterpret_cast<uint32_t*>(ws + kWorkspaceHeader + align256(m * slices * kZSlice * 2) +
+                                           align256(w->n * (w->k / kNf4Block) * 4));
+    p.ce = call_epoch_of(ws);
   }
   p.mtiles = int((m + wide::kBM - 1) / wide::kBM);
-  const dim3 grid(unsigned(p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN)));
+  // LoRA launches put one z producer per M-tile ahead of the GEMM tiles.
+  const dim3 grid(unsigned(p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN) + (lora ? p.mtiles : 0)));
   if (lora) hipLaunchKernelGGL((wide::gemm_kernel<true>), grid, dim3(wide::kThreads), 0, s, p);
   else hipLaunchKernelGGL((wide::gemm_kernel<false>), grid, dim3(wide::kThreads), 0, s, p);
   LF_HIP(hipGetLastError());
