@@ -294,6 +294,7 @@ def main() -> int:
     parser.add_argument("--only", action="store_true", help="headline decode only (no sweep/prefill/CPU)")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-prefill", action="store_true")
+    parser.add_argument("--prefill-only", action="store_true", help="c5 prefill only (JSON of its timings)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -305,6 +306,11 @@ def main() -> int:
     import torch
 
     device = torch.device("cuda:0")
+    if args.prefill_only:
+        pre = run_prefill(device)
+        log(f"prefill c5: {pre['fused']['us_per_call']:.1f} us/call, {pre['fused']['tflops']:.1f} TFLOP/s ({pre['fused']['frac']:.1%})")
+        print(json.dumps(pre), flush=True)
+        return 0
     log(f"device {torch.cuda.get_device_name(0)}; building {LAYERS} weight/adapter copies")
     work = DecodeWorkload(device)
     log(f"headline decode B={args.batch}: warmup {args.warmup}, steps {args.steps}")

@@ -140,7 +140,8 @@ constexpr int kXCopies = kXBytes / 1024 / (kThreads / 64);  // 16-byte copies pe
 constexpr int kDw = kBN * 8 / kThreads;  // packed W dwords per lane and stage
 constexpr int kJ = 3;                    // 16-column fragments per wave
 static_assert(kBN * 8 % kThreads == 0 && kXBytes % (1024 * (kThreads / 64)) == 0, "tile split");
-static_assert(kXD * kXBytes + 2 * kWBytes + 2048 <= 160 * 1024, "LDS budget");
+static_assert(kXD * kXBytes + 2 * kWBytes + 2048 + 12 * 1024 <= 160 * 1024, "LDS budget (codebook pairs, LoRA tables)");
+static_assert(kThreads == 512, "one codebook-pair float per thread");
 
 // Packed W dwords and fp32 block scales of one k-step, loaded without
 // compiler tracking (the x copies in flight would otherwise make every use of
@@ -196,38 +197,36 @@ __device__ __forceinline__ void ldsw128(uint32_t addr, const u32x4& v) {
 
 // Decode of one loaded step into a decoded-W stage, in two halves: the
 // codebook lookups of all dwords, then the scaling, rounding and the stores.
-// The codebook sits 256-byte aligned in LDS, so a lookup address is the table
-// address with its low byte replaced by 4 * nibble (one byte permute).
+// The codebook sits in LDS as a byte -> (code[hi nibble], code[lo nibble])
+// table of fp32 pairs (2 KiB, 2 KiB-aligned), so one 8-byte read returns the
+// two codes of a packed byte.
 struct Looked {
   float v[kDw][8];
 };
 
-// Lookup addresses: byte b of `even` / `odd` holds 4 * the high / low nibble
-// of packed byte b.
 struct LookAddr {
-  uint32_t a[kDw][8];
+  uint32_t a[kDw][4];  // table address of packed byte b of dword i
 };
 
 __device__ __forceinline__ void lookup_addresses(const Packed& w, uint32_t table_addr, LookAddr& la) {
 #pragma unroll
   for (int i = 0; i < kDw; ++i) {
     const uint32_t d = w.q[i];
-    const uint32_t even = (d >> 2) & 0x3c3c3c3cu;
-    const uint32_t odd = (d << 2) & 0x3c3c3c3cu;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      // Byte 0 from byte b of the first operand, bytes 1..3 from the table address.
-      const uint32_t sel = 0x03020100u | (4u + b);
-      la.a[i][2 * b] = __builtin_amdgcn_perm(even, table_addr, sel);
-      la.a[i][2 * b + 1] = __builtin_amdgcn_perm(odd, table_addr, sel);
-    }
+    la.a[i][0] = ((d << 3) & 0x7f8u) | table_addr;
+    la.a[i][1] = ((d >> 5) & 0x7f8u) | table_addr;
+    la.a[i][2] = ((d >> 13) & 0x7f8u) | table_addr;
+    la.a[i][3] = ((d >> 21) & 0x7f8u) | table_addr;
   }
 }
 
-// The 8 lookups of dword i.
+// The 4 lookups of dword i (its 8 elements in order).
 __device__ __forceinline__ void lookup_dword(const LookAddr& la, int i, Looked& lk) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) lk.v[i][e] = lds_read32f(la.a[i][e]);
+  for (int b = 0; b < 4; ++b) {
+    const u32x2 v = lds_read64(la.a[i][b]);
+    lk.v[i][2 * b] = __uint_as_float(v.x);
+    lk.v[i][2 * b + 1] = __uint_as_float(v.y);
+  }
 }
 
 __device__ __forceinline__ void tie_lookups(Looked& lk) {
@@ -466,7 +465,7 @@ template <bool kLora>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) char xring[kXD * kXBytes];
   __shared__ __attribute__((aligned(16))) uint4 wdec[2][kBN * 8];
-  __shared__ __attribute__((aligned(256))) float table[16];
+  __shared__ __attribute__((aligned(2048))) float table[512];  // [byte] -> (code[byte >> 4], code[byte & 15])
   __shared__ __attribute__((aligned(16))) int tslot[kLora ? kBM : 1];
   __shared__ int list[kLora ? kMaxList + 1 : 1];
   __shared__ int cum[kLora ? kMaxList + 1 : 1];
@@ -514,7 +513,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   issue_x(p, xring, m0, 0, wave, lane);
   issue_w(p, min(1, nk - 1), wl, wa);
   issue_x(p, xring + kXBytes, m0, min(1, nk - 1), wave, lane);
-  if (tid < 16) table[tid] = sload(p.code, tid);
+  table[tid] = sload(p.code, (tid & 1) ? (tid >> 1) & 15 : tid >> 5);
   __syncthreads();  // codebook staged
   const uint32_t table_addr = lds_addr(table);
   // Decoded-W store address of this lane (slot 0): row tid >> 3, unit tid & 7.
