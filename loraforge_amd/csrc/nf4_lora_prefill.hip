@@ -58,6 +58,7 @@ struct PrefillParams {
   const int32_t* slice_offsets;
   int slices;
   uint16_t* zpad;     // [m][slices * 64]
+  int y_vec;          // y rows allow 8-byte stores (stride % 4 == 0, 8-byte aligned)
   uint32_t* zflags;   // [mtiles]: the call's tag once the tile's z rows are stored
   CallEpoch ce;
   int mtiles;
@@ -459,6 +460,24 @@ __device__ __forceinline__ void depart(const PrefillParams& p, uint32_t tag) {
   }
 }
 
+// bf16 rounding of the contraction, then of the bias add:
+// acc[i][j][e] holds feature wn0 + 16j + 4g + e.
+__device__ __forceinline__ void round_bias(const PrefillParams& p, f32x4 (&acc)[8][kJ], int wn0, int g) {
+#pragma unroll
+  for (int j = 0; j < kJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int n = wn0 + j * 16 + 4 * g + e;
+      const float bias = (p.bias && n < p.n) ? bf16_to_f32(p.bias[n]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float v = round_bf16(acc[i][j][e]);
+        if (p.bias) v = round_bf16(v + bias);
+        acc[i][j][e] = v;
+      }
+    }
+}
+
 // Block ids below mtiles (LoRA launches only) produce the tiles' z rows;
 // the others are GEMM tiles, M-tile b % mtiles on consecutive ids.
 template <bool kLora>
@@ -609,11 +628,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
     for (int i = 0; i < kDw; ++i) {
       lookup_dword(la, i, lk);
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a0[i]), vec_bf16x8(b0[j]), acc[i][j]);
+      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(b0[j]), vec_bf16x8(a0[i]), acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) acc[kDw][j] = mfma16(vec_bf16x8(a0[kDw]), vec_bf16x8(b0[j]), acc[kDw][j]);
+    for (int j = 0; j < kJ; ++j) acc[kDw][j] = mfma16(vec_bf16x8(b0[j]), vec_bf16x8(a0[kDw]), acc[kDw][j]);
     __builtin_amdgcn_sched_barrier(0);
     // Scaling, rounding and stores of W(kt + 1) over the remaining MFMAs.
     wait_lgkm<0>();  // the lookups (and the k-half-1 fragments before them)
@@ -625,7 +644,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = kDw + 1; i < 8; ++i)
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a0[i]), vec_bf16x8(b0[j]), acc[i][j]);
+      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(b0[j]), vec_bf16x8(a0[i]), acc[i][j]);
     decode_store(dec, lk, wdst + uint32_t(((kt + 1) & 1) * kWBytes));
 #pragma unroll
     for (int q = 0; q < (8 - kDw - 1) * kJ; ++q) {
@@ -642,7 +661,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a1[i]), vec_bf16x8(b1[j]), acc[i][j]);
+      for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(b1[j]), vec_bf16x8(a1[i]), acc[i][j]);
   };
   for (int kt = 0; kt < nk; kt += 2) {
     step(kt, wa, wb);
@@ -651,57 +670,50 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   wait_lgkm<0>();  // the fragment reads past the end
   wait_vm<0>();  // the requests past the end
 
-  // ---- epilogue: acc[i][j][e] = C[token m0 + wm*128 + 16i + 4g + e][feature n0 + wn*48 + 16j + c]
+  // ---- epilogue: acc[i][j][e] = C[token m0 + wm*128 + 16i + c][feature n0 + wn*48 + 16j + 4g + e]
+  // (W is the MFMA's A operand, so a lane holds four consecutive features of
+  // one token: one 8-byte store per fragment).
   const int wn0 = n0 + wn * 48;
-  // LoRA: the z rows of slice 0 and the B fragments of the first slot are
-  // requested before the base rounding, so their latency overlaps it.
-  const int nd = kLora ? list[kMaxList] : 0;
-  const int zw = p.slices * kZSlice;
-  constexpr int kZq = kBM * 8 / kThreads;  // 16-byte z units per thread and slice
-  uint4 zr[kZq];
-  bf16x8 lb0[kJ], lb1[kJ];
-  // B fragments of slot d for this wave's columns: k-group g of ranks 0..31 and 32..63.
-  auto load_b = [&](int d) {
-    const int br = mstride[d];
-    const uint16_t* bg = p.b_store + mboff[d];
-    const bool two = mrank[d] > 32;
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int n = wn0 + j * 16 + c;
-      uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-      if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, g * 8, br);
-      if (two && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + g * 8, br);
-      lb0[j] = as_bf16x8(v0);
-      lb1[j] = as_bf16x8(v1);
-    }
-  };
-  auto load_zs = [&](int s) {
-#pragma unroll
-    for (int q = 0; q < kZq; ++q) {
-      const int row = (tid >> 3) + (kThreads / 8) * q;
-      zr[q] = make_uint4(0, 0, 0, 0);
-      if (tslot[row] >= 0) zr[q] = load_z16(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + (tid & 7) * 8);
-    }
-  };
   if constexpr (kLora) {
+    // z rows of slice 0 and the B fragments of the first slot are requested
+    // before the base rounding, so their latency overlaps it.
+    const int nd = list[kMaxList];
+    const int zw = p.slices * kZSlice;
+    constexpr int kZq = kBM * 8 / kThreads;  // 16-byte z units per thread and slice
+    uint4 zr[kZq];
+    auto load_zs = [&](int s) {
+#pragma unroll
+      for (int q = 0; q < kZq; ++q) {
+        const int row = (tid >> 3) + (kThreads / 8) * q;
+        zr[q] = make_uint4(0, 0, 0, 0);
+        if (tslot[row] >= 0) zr[q] = load_z16(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + (tid & 7) * 8);
+      }
+    };
+    // B fragments of slot d as the MFMA's A operand: feature wn0 + 16j + c,
+    // k-group g of ranks 0..31 (l0) and 32..63 (l1).
+    auto load_b = [&](int d, bf16x8 (&l0)[kJ], bf16x8 (&l1)[kJ]) {
+      const int br = mstride[d];
+      const uint16_t* bg = p.b_store + mboff[d];
+      const bool two = mrank[d] > 32;
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int n = wn0 + j * 16 + c;
+        uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+        if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, g * 8, br);
+        if (two && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + g * 8, br);
+        l0[j] = as_bf16x8(v0);
+        l1[j] = as_bf16x8(v1);
+      }
+    };
+    bf16x8 l0[kJ], l1[kJ];  // B fragments of the slot being applied (slot 0 first)
     wait_z(p, mt, tag);
     load_zs(0);
-    if (nd > 0) load_b(0);
-  }
+    if (nd > 0) load_b(0, l0, l1);
+    round_bias(p, acc, wn0, g);
+    // Routes of this lane's eight tokens.
+    int rslot[8];
 #pragma unroll
-  for (int j = 0; j < kJ; ++j) {
-    const int n = wn0 + j * 16 + c;
-    const float bias = (p.bias && n < p.n) ? bf16_to_f32(p.bias[n]) : 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float v = round_bf16(acc[i][j][e]);
-        if (p.bias) v = round_bf16(v + bias);
-        acc[i][j][e] = v;
-      }
-  }
-  if constexpr (kLora) {
+    for (int i = 0; i < 8; ++i) rslot[i] = tslot[wm * 128 + i * 16 + c];
     uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle (the ring is idle)
     for (int s = 0; s < p.slices; ++s) {
       const int lo = p.slice_offsets[s];
@@ -714,54 +726,66 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       for (int q = 0; q < kZq; ++q) zs[swz((tid >> 3) + (kThreads / 8) * q, tid & 7)] = zr[q];
       __syncthreads();
       if (hi <= wn0 || lo >= wn0 + 48) continue;  // this wave's 48 columns miss the slice
+      const bool inside = lo <= wn0 && wn0 + 48 <= hi;
+      // delta[n][m] = sum_j B_g[n][j] z[m][j] for the wave's 128 tokens x 48
+      // features, added with the reference's two roundings to the tokens
+      // routed to g and the features of slice s.
       for (int d = 0; d < nd; ++d) {
         const int gd = list[d];
-        // Bit 4i + e: the lane's row wm*128 + 16i + 4g + e is routed to gd.
-        uint32_t mine = 0;
+        bool any = false;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int4 ts = *reinterpret_cast<const int4*>(tslot + wm * 128 + i * 16 + 4 * g);
-          mine |= (uint32_t(ts.x == gd) | uint32_t(ts.y == gd) << 1 | uint32_t(ts.z == gd) << 2 |
-                   uint32_t(ts.w == gd) << 3)
-                  << (4 * i);
-        }
-        if (__ballot(mine != 0) == 0) continue;  // none of this wave's 128 rows takes gd
-        if (d > 0 || s > 0) load_b(d);
+        for (int i = 0; i < 8; ++i) any |= rslot[i] == gd;
+        if (__ballot(any) == 0) continue;  // none of this wave's tokens takes slot d
+        if (d > 0 || s > 0) load_b(d, l0, l1);
         const bool two = mrank[d] > 32;
         const float scale = mscale[d];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          if (__ballot((mine >> (4 * i)) & 15u) == 0) continue;  // no row of this 16-row block takes gd
+          const bool mine = rslot[i] == gd;
+          if (__ballot(mine) == 0) continue;  // no token of this 16-row block takes gd
           const int arow = wm * 128 + i * 16 + c;
           const bf16x8 z0 = as_bf16x8(zs[swz(arow, g)]);
           const bf16x8 z1 = as_bf16x8(zs[swz(arow, 4 + g)]);
 #pragma unroll
           for (int j = 0; j < kJ; ++j) {
             f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
-            dacc = mfma16(z0, lb0[j], dacc);
-            if (two) dacc = mfma16(z1, lb1[j], dacc);
-            const int n = wn0 + j * 16 + c;
-            const bool col = n >= lo && n < hi;
+            dacc = mfma16(l0[j], z0, dacc);
+            if (two) dacc = mfma16(l1[j], z1, dacc);
+            if (!mine) continue;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (col && ((mine >> (4 * i + e)) & 1u)) acc[i][j][e] = round_bf16(acc[i][j][e] + round_bf16(dacc[e] * scale));
+            for (int e = 0; e < 4; ++e) {
+              const int n = wn0 + j * 16 + 4 * g + e;
+              if (inside || (n >= lo && n < hi))
+                acc[i][j][e] = round_bf16(acc[i][j][e] + round_bf16(dacc[e] * scale));
+            }
           }
         }
       }
     }
+  } else {
+    round_bias(p, acc, wn0, g);
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 8; ++i) {
+    const int m = m0 + wm * 128 + i * 16 + c;
+    if (m >= p.m) continue;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = m0 + wm * 128 + i * 16 + 4 * g + e;
-      if (m >= p.m) continue;
-#pragma unroll
-      for (int j = 0; j < kJ; ++j) {
-        const int n = wn0 + j * 16 + c;
-        if (n < p.n) p.y[int64_t(m) * p.y_stride + n] = uint16_t(f32_to_bf16(acc[i][j][e]));
+    for (int j = 0; j < kJ; ++j) {
+      const int n = wn0 + j * 16 + 4 * g;  // N % 64 == 0: n < N covers n + 3
+      if (n >= p.n) continue;
+      uint16_t* dst = p.y + int64_t(m) * p.y_stride + n;
+      const uint32_t lo = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+      const uint32_t hi = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
+      if (p.y_vec) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+      } else {
+        dst[0] = uint16_t(lo);
+        dst[1] = uint16_t(lo >> 16);
+        dst[2] = uint16_t(hi);
+        dst[3] = uint16_t(hi >> 16);
       }
     }
+  }
   if constexpr (kLora) depart(p, tag);
 }
 
@@ -814,6 +838,7 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   p.bias = bias;
   p.y = y;
   p.y_stride = y_stride;
+  p.y_vec = (y_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) ? 1 : 0;
   p.slices = slices;
   if (lora) {
     p.a_store = lora->a_store;
