@@ -257,14 +257,18 @@ static_assert(kDw == 3, "decode_store writes three rows");
 // Copies of x k-step kt into a ring stage: position P (16-byte unit) of the
 // 32 KiB stage -> row P / 8, slot P % 8 holding unit (P % 8) ^ (row & 7).
 // Rows past M are clamped (their results are never stored).
+// (32-bit byte offsets from x, so the copies take a scalar base: the
+// launcher checks that x spans less than 4 GiB.)
 __device__ __forceinline__ void issue_x(const PrefillParams& p, char* stage, int m0, int kt, int wave, int lane) {
+  const char* xk = reinterpret_cast<const char*>(p.x) + kt * (kBK * 2);
 #pragma unroll
   for (int d = 0; d < kXCopies; ++d) {
     const int pos = (wave * kXCopies + d) * 64 + lane;
     const int row = pos >> 3;
     const int u = (pos & 7) ^ (row & 7);
     const int tok = min(m0 + row, p.m - 1);
-    copy16(p.x + int64_t(tok) * p.x_stride + kt * kBK + u * 8, stage + (wave * kXCopies + d) * 1024);
+    const uint32_t off = uint32_t(tok) * uint32_t(p.x_stride) * 2u + uint32_t(u) * 16u;
+    copy16(xk + off, stage + (wave * kXCopies + d) * 1024);
   }
 }
 
@@ -610,19 +614,19 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
     issue_w(p, kr, wl, ld);
     issue_x(p, xring + ((kt + 2) % kXD) * kXBytes, m0, kr, wave, lane);
     u32x4 a1[8], b1[kJ];
-    read_half(kt, 1, a1, b1);
     // W(kt + 1) was requested before x(kt + 1) and this step's requests.
     wait_vm<kW + 2 * kXCopies>();
     tie_w(dec);
     LookAddr la;
     lookup_addresses(dec, table_addr, la);
-    wait_lgkm<kHalfReads>();  // the k-half-0 fragments
+    wait_lgkm<0>();  // the k-half-0 fragments
 #pragma unroll
     for (int i = 0; i < 8; ++i) tie(a0[i]);
 #pragma unroll
     for (int j = 0; j < kJ; ++j) tie(b0[j]);
     __builtin_amdgcn_sched_barrier(0);
-    // The lookups between the first k-half-0 MFMAs.
+    // The lookups between the first k-half-0 MFMAs, then the k-half-1
+    // fragment reads (queued behind the lookups; the barrier completes them).
     Looked lk;
 #pragma unroll
     for (int i = 0; i < kDw; ++i) {
@@ -633,14 +637,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
     }
 #pragma unroll
     for (int j = 0; j < kJ; ++j) acc[kDw][j] = mfma16(vec_bf16x8(b0[j]), vec_bf16x8(a0[kDw]), acc[kDw][j]);
+    read_half(kt, 1, a1, b1);
     __builtin_amdgcn_sched_barrier(0);
-    // Scaling, rounding and stores of W(kt + 1) over the remaining MFMAs.
-    wait_lgkm<0>();  // the lookups (and the k-half-1 fragments before them)
+    wait_lgkm<kHalfReads>();  // the lookups
     tie_lookups(lk);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) tie(a1[i]);
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) tie(b1[j]);
 #pragma unroll
     for (int i = kDw + 1; i < 8; ++i)
 #pragma unroll
@@ -653,10 +653,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
     // x(kt + 1) has landed once at most this step's requests are outstanding;
-    // the barrier publishes it with the decoded W(kt + 1), and frees the
-    // slots read at kt - 1 for the requests of step kt + 1.
+    // the barrier publishes it with the decoded W(kt + 1), completes this
+    // wave's k-half-1 fragment reads and frees the slots read at kt - 1 for
+    // the requests of step kt + 1.
     wait_vm<kW + kXCopies>();
     lds_barrier();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tie(a1[i]);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) tie(b1[j]);
     read_half(kt + 1, 0, a0, b0);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -813,6 +818,7 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   const int64_t need = prefill_workspace_bytes(m, w->n, w->k, slices, lora ? lora->max_rank : 1);
   LF_REQUIRE(!(lora || dq) || (workspace && workspace_bytes >= need && aligned16(workspace)),
              "workspace too small: need %lld bytes", (long long)need);
+  LF_REQUIRE((m - 1) * x_stride * 2 + w->k * 2 < (int64_t(1) << 32), "x spans 4 GiB or more");
   auto s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   const float* scales = w->scales;
