@@ -219,6 +219,36 @@ def test_prefill_slices_and_interleaved_routes(device):
     close(bits(y), _cases.fused_expected(case))
 
 
+def test_prefill_repeated_calls_and_graph_replay(device):
+    """The in-launch z producers publish per call (call-epoch tags): eager repeats and graph replays agree."""
+    m = 600  # three token tiles, the last one ragged
+    slots = np.repeat(np.array([2, 0, -1, 1, 0], np.int32), [150, 130, 40, 200, 80])
+    case = _cases.fused_case(m, 448, 512, ranks=(16, 32, 8), seed=41, token_slots=slots)
+    x, q, st, lora, _ = to_device(case, device)
+    expect = _cases.fused_expected(case)
+    out = torch.empty(m, 448, dtype=torch.bfloat16, device=device)
+    for _ in range(3):
+        nf4_lora_linear(x, q, st, lora=lora, out=out)
+    torch.cuda.synchronize()
+    close(bits(out), expect)
+    eager = out.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        nf4_lora_linear(x, q, st, lora=lora, out=out)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            nf4_lora_linear(x, q, st, lora=lora, out=out)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 def test_prefill_c5_shape_sampled(device):
     m, n, k = 2048, 11008, 4096
     rng = np.random.default_rng(735)
