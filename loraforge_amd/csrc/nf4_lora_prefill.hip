@@ -757,11 +757,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
             dacc = mfma16(l0[j], z0, dacc);
             if (two) dacc = mfma16(l1[j], z1, dacc);
             if (!mine) continue;
+            // bf16(scale * delta) for the four features at once; the sum with
+            // the rounded base is rounded once more by the output store.
+            const uint32_t t01 = pack_bf16x2(dacc[0] * scale, dacc[1] * scale);
+            const uint32_t t23 = pack_bf16x2(dacc[2] * scale, dacc[3] * scale);
+            const float t[4] = {bf16_lo(t01), bf16_hi(t01), bf16_lo(t23), bf16_hi(t23)};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int n = wn0 + j * 16 + 4 * g + e;
-              if (inside || (n >= lo && n < hi))
-                acc[i][j][e] = round_bf16(acc[i][j][e] + round_bf16(dacc[e] * scale));
+              if (inside || (n >= lo && n < hi)) acc[i][j][e] += t[e];
             }
           }
         }
