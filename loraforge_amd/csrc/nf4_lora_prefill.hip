@@ -58,7 +58,7 @@ struct PrefillParams {
   const int32_t* slice_offsets;
   int slices;
   uint16_t* zpad;     // [m][slices * 64]
-  int y_vec;          // y rows allow 8-byte stores (stride % 4 == 0, 8-byte aligned)
+  int y_vec;          // 2: 16-byte aligned y rows, 1: 8-byte aligned, 0: neither
   uint32_t* zflags;   // [mtiles]: the call's tag once the tile's z rows are stored
   CallEpoch ce;
   int mtiles;
@@ -774,24 +774,55 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   } else {
     round_bias(p, acc, wn0, g);
   }
+  if (p.y_vec == 2) {
+    // 16-byte aligned rows: the tile goes through LDS (the idle x ring, rows
+    // of 384 bytes, 16-byte chunks XOR-swizzled by row & 7) and leaves as
+    // whole rows, so each 128-byte line of y is written by one request.
+    static_assert(kBN * 2 == 384 && kBM * 384 <= kXD * kXBytes, "output staging fits the x ring");
+    __syncthreads();  // every wave is done with the ring
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int m = m0 + wm * 128 + i * 16 + c;
-    if (m >= p.m) continue;
+    for (int i = 0; i < 8; ++i) {
+      const int row = wm * 128 + i * 16 + c;
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int n = wn0 + j * 16 + 4 * g;  // N % 64 == 0: n < N covers n + 3
-      if (n >= p.n) continue;
-      uint16_t* dst = p.y + int64_t(m) * p.y_stride + n;
-      const uint32_t lo = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
-      const uint32_t hi = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
-      if (p.y_vec) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
-      } else {
-        dst[0] = uint16_t(lo);
-        dst[1] = uint16_t(lo >> 16);
-        dst[2] = uint16_t(hi);
-        dst[3] = uint16_t(hi >> 16);
+      for (int j = 0; j < kJ; ++j) {
+        const int q = wn * 6 + 2 * j + (g >> 1);  // 16-byte chunk of the row
+        const uint32_t lo = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+        const uint32_t hi = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
+        *reinterpret_cast<uint2*>(xring + row * 384 + ((q ^ (row & 7)) << 4) + (g & 1) * 8) = make_uint2(lo, hi);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kBM * 24 / kThreads; ++r) {
+      const int id = tid + r * kThreads;
+      const int row = id / 24;
+      const int q = id - row * 24;
+      const int m = m0 + row;
+      const int n = n0 + q * 8;
+      if (m < p.m && n < p.n)
+        *reinterpret_cast<uint4*>(p.y + int64_t(m) * p.y_stride + n) =
+            *reinterpret_cast<const uint4*>(xring + row * 384 + ((q ^ (row & 7)) << 4));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = m0 + wm * 128 + i * 16 + c;
+      if (m >= p.m) continue;
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) {
+        const int n = wn0 + j * 16 + 4 * g;  // N % 64 == 0: n < N covers n + 3
+        if (n >= p.n) continue;
+        uint16_t* dst = p.y + int64_t(m) * p.y_stride + n;
+        const uint32_t lo = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+        const uint32_t hi = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
+        if (p.y_vec) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+        } else {
+          dst[0] = uint16_t(lo);
+          dst[1] = uint16_t(lo >> 16);
+          dst[2] = uint16_t(hi);
+          dst[3] = uint16_t(hi >> 16);
+        }
       }
     }
   }
@@ -848,7 +879,9 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   p.bias = bias;
   p.y = y;
   p.y_stride = y_stride;
-  p.y_vec = (y_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) ? 1 : 0;
+  p.y_vec = (y_stride % 8 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0) ? 2
+            : (y_stride % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0)  ? 1
+                                                                                 : 0;
   p.slices = slices;
   if (lora) {
     p.a_store = lora->a_store;
