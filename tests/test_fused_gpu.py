@@ -219,6 +219,22 @@ def test_prefill_slices_and_interleaved_routes(device):
     close(bits(y), _cases.fused_expected(case))
 
 
+@pytest.mark.parametrize("offset", [8, 4, 1])
+def test_prefill_strided_output(offset, device):
+    """Output rows 16-, 8- and 2-byte aligned (column views of a wider tensor): all three store paths."""
+    m, n = 300, 384
+    slots = np.repeat(np.array([1, -1, 0], np.int32), [120, 30, 150])
+    case = _cases.fused_case(m, n, 256, ranks=(16, 8), seed=90 + offset, token_slots=slots, bias=True)
+    x, q, st, lora, bias = to_device(case, device)
+    big = torch.full((m, n + 24), -7.0, dtype=torch.bfloat16, device=device)
+    out = big[:, offset : offset + n]
+    nf4_lora_linear(x, q, st, bias=bias, lora=lora, out=out)
+    torch.cuda.synchronize()
+    close(bits(out), _cases.fused_expected(case))
+    # Nothing outside the view was written.
+    assert torch.all(big[:, :offset] == -7.0) and torch.all(big[:, offset + n :] == -7.0)
+
+
 def test_prefill_repeated_calls_and_graph_replay(device):
     """The in-launch z producers publish per call (call-epoch tags): eager repeats and graph replays agree."""
     m = 600  # three token tiles, the last one ragged
