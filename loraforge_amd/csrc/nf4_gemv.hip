@@ -514,14 +514,27 @@ __device__ __forceinline__ B8 b8_at(const GemvParams& p, int64_t boff, int st, i
   return b;
 }
 
+// The first cnt bf16 elements of v, the rest zero.
+__device__ __forceinline__ uint4 keep_first(const uint4& v, int cnt) {
+  uint32_t o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = 2 * k >= cnt ? 0u : 2 * k + 1 >= cnt ? (o[k] & 0xffffu) : o[k];
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Dword i of v (0 past the end), by selects: a runtime-indexed array would
+// live in scratch.
+__device__ __forceinline__ uint32_t dword_at(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : i == 3 ? v.w : 0u;
+}
+
 __device__ __forceinline__ uint4 b8_fix(const uint4& v, const B8& b) {
-  const uint32_t w[5] = {v.x, v.y, v.z, v.w, 0u};
   const int d = b.off >> 1;
   uint32_t out[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t a = k + d < 4 ? w[k + d < 4 ? k + d : 4] : 0u;
-    const uint32_t c = k + d + 1 < 4 ? w[k + d + 1 < 4 ? k + d + 1 : 4] : 0u;
+    const uint32_t a = dword_at(v, k + d);
+    const uint32_t c = dword_at(v, k + d + 1);
     uint32_t o = (b.off & 1) ? ((a >> 16) | (c << 16)) : a;
     if (2 * k >= b.cnt) o = 0u;
     else if (2 * k + 1 >= b.cnt) o &= 0xffffu;
@@ -693,15 +706,18 @@ __device__ void lora_gather(const GemvParams& p, char* lds, int t0, int mt, uint
 // wave w takes the tile's distinct slots w, w + 7, ...; for each, delta[token][column] += z[token][s*64 + j] * B_g[column][j]
 // over ranks in steps of 32, with z rows of other slots' tokens masked to
 // zero, into tiles of the base layout (token rows x 16 columns). Columns of
-// other slices are masked on the B side. B fragments go four slots at a
-// time; the first batch is requested by expand_b_first as soon as a wave
-// has finished its contraction (the slot list is published before the wait
-// for z), so its latency overlaps that wait.
+// other slices are masked on the B side. B fragments go kSlotBatch slots
+// at a time, so one batch covers the at most 32 distinct slots of a tile;
+// it is requested as soon as the wave has finished its contraction and is
+// shifted and masked (expand_b_fix) before the wait for z, so both its
+// latency and that VALU work overlap the wait.
 constexpr int kExpandWaves = kWaves - 1;
+constexpr int kSlotBatch = 5;
+static_assert(kSlotBatch * kExpandWaves >= 32, "one batch covers a tile's distinct slots");
 
 template <class TL>
 struct ExpandB {
-  uint4 bf[4][TL::kRT];  // ranks 0..31 (ranks 32..63 are loaded where used)
+  uint4 bf[kSlotBatch][TL::kRT];  // ranks 0..31 (ranks 32..63 are loaded where used)
 };
 
 template <class TL>
@@ -711,7 +727,7 @@ __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMe
   const int kg = lane >> 4;
   const int nd = tm->nd;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < kSlotBatch; ++q) {
     const int d = d0 + q * kExpandWaves;
     const bool live = d < nd;
     const int dd = live ? d : 0;
@@ -721,6 +737,34 @@ __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMe
       // fragments are used, so nothing waits for these loads here.
       b.bf[q][r] = *reinterpret_cast<const uint4*>(
           b8_at(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row0 + r * 16 + n, 8 * kg, live).src);
+  }
+}
+
+// Shifts and masks a landed batch in place (b8_fix with the addresses the
+// loads used): ranks 0..31 of each slot, ready for the MFMAs. The contraction
+// waves do this before waiting for z, so the VALU work is off the path.
+template <class TL>
+__device__ __forceinline__ void expand_b_fix(const GemvParams& p, const TileMeta* tm, ExpandB<TL>& b, int d0,
+                                             int row0, int lane) {
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+  const int nd = tm->nd;
+#pragma unroll
+  for (int q = 0; q < kSlotBatch; ++q) {
+    const int d = d0 + q * kExpandWaves;
+    if (d >= nd) break;  // uniform
+    const int st = tm->dstride[d];
+    const int cnt = min(8, tm->dr[d] - 8 * kg);  // elements kept (<= 0: none)
+    if (st >= 8) {
+      // Aligned rows (the common case): only the elements past the rank go.
+#pragma unroll
+      for (int r = 0; r < TL::kRT; ++r) b.bf[q][r] = keep_first(b.bf[q][r], cnt);
+    } else {
+      const int boff = int(tm->dboff[d] & 7);
+#pragma unroll
+      for (int r = 0; r < TL::kRT; ++r)
+        b.bf[q][r] = b8_fix(b.bf[q][r], B8{nullptr, (boff + (row0 + r * 16 + n) * st + 8 * kg) & 7, cnt});
+    }
   }
 }
 
@@ -757,10 +801,13 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
   }
   const int s_lo = int(p.slices > 1 && row0 >= bounds[1]) + int(p.slices > 2 && row0 >= bounds[2]);
   const int s_hi = int(p.slices > 1 && row0 + TL::kR - 1 >= bounds[1]) + int(p.slices > 2 && row0 + TL::kR - 1 >= bounds[2]);
-  for (int d0 = wave; d0 < nd; d0 += 4 * kExpandWaves) {
-    if (d0 != wave) expand_b_batch<TL>(p, tm, b, d0, row0, lane);
+  for (int d0 = wave; d0 < nd; d0 += kSlotBatch * kExpandWaves) {
+    if (d0 != wave) {
+      expand_b_batch<TL>(p, tm, b, d0, row0, lane);
+      expand_b_fix<TL>(p, tm, b, d0, row0, lane);
+    }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kSlotBatch; ++q) {
       const int d = d0 + q * kExpandWaves;
       if (d >= nd) break;  // uniform
       const int g = tm->dslot[d];
@@ -779,9 +826,12 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
           }
 #pragma unroll
           for (int r = 0; r < RT; ++r) {
-            const B8 b8 = b8_at(p, tm->dboff[d], tm->dstride[d], rk, row0 + r * 16 + n, 32 * h + 8 * kg, true);
-            const uint4 raw = h == 0 ? b.bf[q][r] : *reinterpret_cast<const uint4*>(b8.src);
-            const uint4 bb = cs[r] == s ? b8_fix(raw, b8) : make_uint4(0, 0, 0, 0);
+            uint4 fixed = b.bf[q][r];  // ranks 0..31: shifted and masked already
+            if (h == 1) {
+              const B8 b8 = b8_at(p, tm->dboff[d], tm->dstride[d], rk, row0 + r * 16 + n, 32 + 8 * kg, true);
+              fixed = b8_fix(*reinterpret_cast<const uint4*>(b8.src), b8);
+            }
+            const uint4 bb = cs[r] == s ? fixed : make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < TT; ++t) dacc[r][t] = mfma16(as_bf16x8(zf[t]), as_bf16x8(bb), dacc[r][t]);
           }
@@ -868,10 +918,10 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
 
   // Weight stages (the contraction waves; blocks clamped into range, so all
   // D stages are always requested). A producing workgroup requests its first
-  // shrink unit's fragments between stage 0 and stage 1 (untracked loads),
-  // so they are not queued behind the whole prologue; they have landed once
-  // stage 1 has, and the contraction waves consume them in their first loop
-  // iteration.
+  // shrink unit's fragments ahead of the stages (untracked loads): at small
+  // batches the D stages are most of the weight stream, and fragments queued
+  // behind them would land only near its end. The contraction waves compute
+  // the unit's partials before their first stage.
   Unit un0{};
   bool has0 = false;
   FirstFrags pre;
@@ -879,13 +929,12 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   uint32_t epoch = 0;
   if (wave < kBase) {
     auto stage_kb = [&](int s) { return min(kb0 + s * TL::kSB, nblk - 1); };
-    issue_stage<TL>(p, myring, row0, t0, mt, stage_kb(0), kend, lane);
     if constexpr (kLora) {
       has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
       if (has0) first_frags(p, un0, wave, lane, pre);
     }
 #pragma unroll
-    for (int s = 1; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
+    for (int s = 0; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
   } else if constexpr (kLora) {
     // The LoRA wave: the epoch and its tile's token metadata.
     epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -939,28 +988,27 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   // are in registers.
   Frags<TL> cur, nxt;
   ExpandB<TL> eb;
-  static_assert((D - 1) * TL::kDma + kBatch + 1 < 64, "vmcnt range");
+  static_assert(D * TL::kDma < 64, "vmcnt range");
+  if constexpr (kLora) {
+    // The unit's fragments were requested before the D stages: they have
+    // landed once only the stages are outstanding.
+    if (wave < kBase && has0) {
+      wait_vm<D * TL::kDma>();
+      first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
+    }
+  }
   if (nst > 0) {
-    // A producing wave requested its unit fragments between stage 0 and
-    // stage 1: stage 0 has landed once only those and the later stages are
-    // outstanding.
-    if (kLora && has0 && nst >= D) wait_vm<(D - 1) * TL::kDma + (kLora ? kBatch + 1 : 0)>();
-    else wait_stages<TL>(min(D - 1, nst - 1));
+    wait_stages<TL>(min(D - 1, nst - 1));
     read_frags<TL>(cur, ring_base, n, g);
     settle(cur);
   }
   // One ring stage: read the next stage's fragments, refill, contract this
   // one.
-  auto step = [&](int s, bool first) {
+  auto step = [&](int s) {
     const bool more = s + 1 < nst;
     if (more) {
       wait_stages<TL>(min(D - 2, nst - 2 - s));
       read_frags<TL>(nxt, ring_base + ((s + 1) % D) * TL::kStage, n, g);
-    }
-    // Stage 1 has landed, so have the first unit's fragments (requested
-    // before it).
-    if constexpr (kLora) {
-      if (first && more && has0) first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
     }
     if (s + D < nst)
       issue_stage<TL>(p, myring + (s % D) * TL::kStage, row0, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
@@ -970,9 +1018,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       cur = nxt;
     }
   };
-  // Stage 0 apart, so that the unit fragments are not live in the loop.
-  if (nst > 0) step(0, true);
-  for (int s = 1; s < nst; ++s) step(s, false);
+  for (int s = 0; s < nst; ++s) step(s);
 
   // Sum the waves' partial tiles: wave w writes its tiles into its own ring
   // (all of its copies have landed), then tile c = wave is summed by wave c.
@@ -992,11 +1038,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       lora_gather<TL>(p, lora7, t0, mt, __builtin_amdgcn_readfirstlane(epoch) + 1u, lane);
       departed = depart_issue(p.ce, lane);  // after the last partial load: nothing waits for it until the end
     } else {
-      if (has0 && nst < 2) {
-        wait_vm<0>();
-        first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
-      }
       expand_b_first<TL>(p, lora7, eb, row0, wave, lane);
+      expand_b_fix<TL>(p, reinterpret_cast<const TileMeta*>(lora7 + LoraLds<TL>::kMeta), eb, wave, row0, lane);
     }
     lds_barrier();  // z and the tile metadata are in LDS
     if (wave < kBase) expand_mfma<TL>(p, lora7, eb, bounds, dacc, row0, wave, lane);
