@@ -252,11 +252,11 @@ struct Unit {
 
 // Unit u's token, adapter rows and k-slice (scalar loads); false when the
 // token has no adapter (base only), so nothing is produced.
-__device__ __forceinline__ bool unit_of(const GemvParams& p, int u, Unit& un) {
+// g: the token's slot, token_slots[u / kz], loaded by the caller.
+__device__ __forceinline__ bool unit_of_slot(const GemvParams& p, int u, int g, Unit& un) {
   un.t = u / p.kz;
   un.ks = u - un.t * p.kz;
   const int ks = un.ks;
-  const int g = sload(p.token_slots, un.t);
   if (g < 0) return false;
   const int r = sload(p.ranks, g);
   if (r <= 0 || r > p.max_rank) return false;
@@ -269,6 +269,10 @@ __device__ __forceinline__ bool unit_of(const GemvParams& p, int u, Unit& un) {
     un.steps = 0;
   }
   return true;
+}
+
+__device__ __forceinline__ bool unit_of(const GemvParams& p, int u, Unit& un) {
+  return unit_of_slot(p, u, sload(p.token_slots, u / p.kz), un);
 }
 
 // Partial of value j of unit (token t, k-slice ks): entry (t * zw + j) * kz +
@@ -439,8 +443,13 @@ __device__ void first_unit_partials(const GemvParams& p, const Unit& un, FirstFr
 __device__ void publish_first_unit(const GemvParams& p, const float* red, const int* done, const Unit& un,
                                    uint32_t tag, int lane) {
   const int rows = un.rows;
-  while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kProd)
+  for (int spins = 0; __hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kProd; ++spins) {
+    if (spins > kSpinLimit) {  // cannot happen (every contraction wave counts in); bounded all the same
+      if (lane == 0) __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
+  }
 #pragma unroll
   for (int q = 0; q < 3; ++q) {
     const int jj = q * 64 + lane;
@@ -568,10 +577,10 @@ struct TokenMeta {
   int64_t boff;
 };
 
-__device__ __forceinline__ TokenMeta token_meta(const GemvParams& p, int t0, int mt, int lane) {
+// g: token_slots[t0 + min(lane, mt - 1)], loaded by the caller.
+__device__ __forceinline__ TokenMeta token_meta(const GemvParams& p, int g, int mt, int lane) {
   TokenMeta m;
-  m.g = p.token_slots[t0 + min(lane, mt - 1)];
-  if (lane >= mt) m.g = -1;
+  m.g = lane < mt ? g : -1;
   const bool live = m.g >= 0;
   const void* fb = p.slice_offsets;
   m.r = *(live ? p.ranks + m.g : static_cast<const int32_t*>(fb));
@@ -927,6 +936,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   FirstFrags pre;
   TokenMeta tmeta{};
   uint32_t epoch = 0;
+  int g_tile = -1, g_unit = -1;  // the LoRA wave: token slots loaded in the prologue
   if (wave < kBase) {
     auto stage_kb = [&](int s) { return min(kb0 + s * TL::kSB, nblk - 1); };
     if constexpr (kLora) {
@@ -936,10 +946,14 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int s = 0; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
   } else if constexpr (kLora) {
-    // The LoRA wave: the epoch and its tile's token metadata.
+    // The LoRA wave: the epoch and the first loads of its metadata chains
+    // (vector loads: the barriers below wait only for scalar loads and LDS,
+    // so the whole workgroup does not wait for these round trips); the
+    // dependent loads follow the barriers.
     epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    tmeta = token_meta(p, t0, mt, lane);
-    has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
+    g_tile = p.token_slots[t0 + min(lane, mt - 1)];
+    const bool producer = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units;
+    g_unit = producer ? p.token_slots[int(blockIdx.x) / p.kz] : -1;
   }
 
   if (threadIdx.x == 0) {
@@ -967,6 +981,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   // the contraction waves have counted in), the other units, then z.
   if constexpr (kLora) {
     if (wave == kBase) {
+      tmeta = token_meta(p, g_tile, mt, lane);
+      has0 = g_unit >= 0 && unit_of_slot(p, blockIdx.x, __builtin_amdgcn_readfirstlane(g_unit), un0);
       const uint32_t tag = __builtin_amdgcn_readfirstlane(epoch) + 1u;
       lora_meta<TL>(lora_lds, tmeta, lane);
       if (has0) publish_first_unit(p, red, &prod_done, un0, tag, lane);
