@@ -151,6 +151,18 @@ int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_
  * tests and diagnostics only (synchronises the stream). */
 int lf_nf4_lora_status(const void* workspace, void* stream, int32_t* status);
 
+/* --------------------------------------------------------------------------
+ * SwiGLU between an MLP's gate/up and down projections (the c3 chain):
+ * out[t, c] = bf16(bf16(silu(g)) * u), g = gate_up[t, c], u = gate_up[t, n + c],
+ * silu(g) = g / (1 + exp(-g)) in fp32. Replaces the activation step of
+ * benchmarks/qwen35_decode_silu.py:60-61 (row_act_kernel) and
+ * benchmarks/qwen35_prefill_fused.py:14-93 (expand_act_kernel), which apply
+ * it after the gate/up LoRA adds; here it reads the merged two-slice output
+ * of lf_nf4_lora_linear. in_stride >= 2n, out_stride >= n (elements).
+ * ------------------------------------------------------------------------ */
+int lf_swiglu(const uint16_t* gate_up, int64_t rows, int64_t n, int64_t in_stride, uint16_t* out,
+              int64_t out_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,6 +101,7 @@ _PROTOTYPES = {
         ],
     ),
     "lf_nf4_lora_status": (ctypes.c_int, [c_void_p, c_void_p, ctypes.POINTER(c_int32)]),
+    "lf_swiglu": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p]),
 }
 
 EXPORTS = tuple(_PROTOTYPES)

@@ -6,6 +6,7 @@ Mirrors the structural rejection cases of the reference
 lengths, thread counts and output aliasing raise before any launch.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -87,3 +88,14 @@ def test_lora_batch_from_padded_offsets():
     )
     assert lb.a_offsets.tolist() == [0, 32 * 64, 2 * 32 * 64]
     assert lb.num_slices == 2 and lb.a_store.ndim == 1
+
+
+def test_silu_mul_rejects_cpu_and_bad_types():
+    from loraforge_amd.ops.activation import silu_mul
+
+    with pytest.raises(ValueError, match="same CUDA"):
+        silu_mul(torch.zeros(2, 16, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="dtype"):
+        silu_mul(torch.zeros(2, 16, dtype=torch.float32))
+    with pytest.raises(TypeError):
+        silu_mul(np.zeros((2, 16)))

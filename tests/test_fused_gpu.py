@@ -302,3 +302,20 @@ def test_decode_after_prefill_on_one_workspace(device):
         head = ws[:2048].view(torch.int32)
         assert int(head[0]) == 2 * call
         assert not head[32:512].any()
+
+
+@pytest.mark.parametrize("dq", [False, True])
+def test_weights_loaded_from_quant_state_file(tmp_path, dq, device):
+    """NF4 weights stored as packed QuantState entries feed the fused call unchanged."""
+    from loraforge_amd.ops.quant_state import load_nf4_weight, save_nf4_weights
+
+    case = _cases.fused_case(8, 256, 512, ranks=(16, 8), double_quant=dq, seed=41)
+    x, q, st, lora, _ = to_device(case, device)
+    path = tmp_path / "w.safetensors"
+    save_nf4_weights(path, {"proj.weight": (q, st)})
+    lq, lst = load_nf4_weight(path, "proj.weight", device=device)
+    y = nf4_lora_linear(x, q, st, lora=lora)
+    y_loaded = nf4_lora_linear(x, lq, lst, lora=lora)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_loaded)
+    close(bits(y_loaded), _cases.fused_expected(case))
