@@ -319,3 +319,23 @@ def test_weights_loaded_from_quant_state_file(tmp_path, dq, device):
     torch.cuda.synchronize()
     assert torch.equal(y, y_loaded)
     close(bits(y_loaded), _cases.fused_expected(case))
+
+
+def test_empty_batch_and_smallest_shapes(device):
+    """Zero tokens launch nothing; K = N = 64 (one NF4 block per row) works on both paths."""
+    case = _cases.fused_case(4, 64, 64, ranks=(16, 64), seed=51, null_frac=0.0)
+    x, q, st, lora, _ = to_device(case, device)
+    empty = nf4_lora_linear(x[:0], q, st)
+    assert empty.shape == (0, 64)
+    for m in (1, 4):
+        sub = dict(case, x=case["x"][:m], m=m)
+        sub["lora"] = dict(case["lora"], token_slots=case["lora"]["token_slots"][:m])
+        xs, _, _, lora_m, _ = to_device(sub, device)
+        y = nf4_lora_linear(xs, q, st, lora=lora_m)
+        torch.cuda.synchronize()
+        close(bits(y), _cases.fused_expected(sub))
+    big = _cases.fused_case(96, 64, 64, ranks=(16, 64), seed=52)
+    x, q, st, lora, _ = to_device(big, device)
+    y = nf4_lora_linear(x, q, st, lora=lora)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(big))
