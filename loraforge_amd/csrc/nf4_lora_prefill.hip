@@ -61,6 +61,7 @@ struct PrefillParams {
   int y_vec;          // 2: 16-byte aligned y rows, 1: 8-byte aligned, 0: neither
   uint32_t* zflags;   // [mtiles]: the call's tag once the tile's z rows are stored
   CallEpoch ce;
+  int* status;  // set to 1 if a wait for z gives up (cannot happen while producers run first)
   int mtiles;
 };
 
@@ -439,8 +440,15 @@ __device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, uint32
 // workgroups' feet.
 __device__ __forceinline__ void wait_z(const PrefillParams& p, int mt, uint32_t tag) {
   if (threadIdx.x == 0) {
-    while (__hip_atomic_load(p.zflags + mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag)
+    // Bounded (about a quarter second): a workgroup never waits forever,
+    // whatever the launch order; giving up is reported in the status word.
+    for (int spins = 0; __hip_atomic_load(p.zflags + mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag; ++spins) {
+      if (spins > (1 << 20)) {
+        __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
       __builtin_amdgcn_s_sleep(8);
+    }
   }
   __syncthreads();
 }
@@ -897,6 +905,7 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.zflags = reinterpret_cast<uint32_t*>(ws + kWorkspaceHeader + align256(m * slices * kZSlice * 2) +
                                            align256(w->n * (w->k / kNf4Block) * 4));
     p.ce = call_epoch_of(ws);
+    p.status = reinterpret_cast<int*>(ws + kStatusOffset);
   }
   p.mtiles = int((m + wide::kBM - 1) / wide::kBM);
   // LoRA launches put one z producer per M-tile ahead of the GEMM tiles.

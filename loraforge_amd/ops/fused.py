@@ -311,7 +311,7 @@ def nf4_lora_linear(
 
 
 def decode_status(workspace=None, device=None) -> int:
-    """Status word of the last decode call on a workspace (0 = ok); synchronises."""
+    """Status word of the fused calls on a workspace (0 = ok; 1 = a wait for z gave up); synchronises."""
     import ctypes
 
     import torch

@@ -183,6 +183,7 @@ def test_prefill_segments(m, dq, device):
     y = nf4_lora_linear(x, q, st, bias=bias, lora=lora)
     torch.cuda.synchronize()
     close(bits(y), _cases.fused_expected(case))
+    workspace_clean(device)
 
 
 @pytest.mark.parametrize("k", [64, 192, 320])
