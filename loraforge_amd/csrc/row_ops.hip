@@ -200,7 +200,7 @@ extern "C" int lf_row_shrink(const uint16_t* x, const uint16_t* a, uint16_t* z, 
   LF_REQUIRE(tokens >= 0 && tokens < (int64_t(1) << 31), "tokens out of range");
   if (tokens == 0) return lf::kOk;
   LF_REQUIRE(x && a && z && slots && ranks, "null pointer argument");
-  LF_REQUIRE(num_slices >= 1 && num_slices <= 3, "num_slices must be in 1..3");
+  LF_REQUIRE(num_slices >= 1 && num_slices <= lf::kMaxSlices, "num_slices must be in 1..4");
   LF_REQUIRE(max_rank >= 1 && max_rank <= 64 && capacity >= max_rank, "max_rank must be in 1..64 and <= capacity");
   LF_REQUIRE(width > 0 && width % 8 == 0 && x_stride >= width && x_stride % 8 == 0 && width < (int64_t(1) << 31),
              "x width and row stride must be multiples of 8");

@@ -3,6 +3,7 @@
 from .fused import LoraBatch, nf4_lora_linear, segments_to_slots, workspace_bytes
 from .lora_rows import row_expand, row_shrink
 from .nf4 import NF4State, NestedState, dequantize_nf4, dequantize_nf4_nested, prepare_scales, quantize_nf4
+from . import rowexpand
 from .quant_state import load_nf4_weight, quant_state_entries, quant_state_from_entries, save_nf4_weights
 
 __all__ = [
@@ -19,6 +20,7 @@ __all__ = [
     "quantize_nf4",
     "row_expand",
     "row_shrink",
+    "rowexpand",
     "save_nf4_weights",
     "segments_to_slots",
     "workspace_bytes",
