@@ -948,8 +948,11 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       // about a microsecond (32 x 64 cycles), so the producers' unit
       // fragments are ahead of it in the memory queues (measured against no
       // delay: B = 1 13.4 -> 12.8 us, B = 8 14.8 -> 14.4 us, B = 64 19.0 ->
-      // 18.7 us; 12 x 64 cycles was worse, 48 x 64 no better).
+      // 18.7 us; 12 x 64 cycles was worse, 48 x 64 no better). Producers
+      // hold their own stages back by half that, behind their fragments
+      // (B = 64 another -0.2 us).
       if (!has0) __builtin_amdgcn_s_sleep(32);
+      else __builtin_amdgcn_s_sleep(16);
     }
 #pragma unroll
     for (int s = 0; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
