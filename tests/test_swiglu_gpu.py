@@ -104,3 +104,37 @@ def test_c3_down_projection_shape(device):
     torch.cuda.synchronize()
     cols = np.unique(np.concatenate([np.arange(0, 4096, 61), [4095]]))
     close(bits(y)[:, cols], _cases.fused_expected(case, rows=cols))
+
+
+def test_c3_chain_graph_replay(mlp_cases, device):
+    """gate/up -> SwiGLU -> down captured in one HIP graph: every replay equals the eager chain."""
+    gate_up_case, down_case = (rows_of(c, 8) for c in mlp_cases)
+    x, q1, st1, lora1, _ = to_device(gate_up_case, device)
+    _, q2, st2, lora2, _ = to_device(dict(down_case, x=np.zeros((8, 3072), np.uint16)), device)
+    gu = torch.empty(8, 6144, dtype=torch.bfloat16, device=device)
+    h = torch.empty(8, 3072, dtype=torch.bfloat16, device=device)
+    y = torch.empty(8, 1024, dtype=torch.bfloat16, device=device)
+
+    def chain():
+        nf4_lora_linear(x, q1, st1, lora=lora1, out=gu)
+        silu_mul(gu, out=h)
+        nf4_lora_linear(h, q2, st2, lora=lora2, out=y)
+
+    chain()
+    torch.cuda.synchronize()
+    eager = y.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        chain()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        chain()
+    for _ in range(3):
+        y.zero_()
+        h.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
