@@ -41,6 +41,10 @@ def test_validation_errors_without_device_work():
         _lib.check(lib.lf_row_expand(*([ctypes.c_void_p(8)] * 12), 4, 4, 4, 1, 4, 64, 64, None))
     with pytest.raises(ValueError, match="num_slices"):
         _lib.check(lib.lf_row_shrink(*([ctypes.c_void_p(16)] * 5), 4, 64, 64, 5, 64, 16, None))
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.check(lib.lf_swiglu(None, 1, 8, 16, None, 8, None))
+    with pytest.raises(ValueError, match="2 \\* n"):
+        _lib.check(lib.lf_swiglu(ctypes.c_void_p(16), 1, 8, 8, ctypes.c_void_p(16), 8, None))
     w = _lib.NF4Weight(n=100, k=64)
     with pytest.raises(ValueError, match="multiples of 64"):
         _lib.check(lib.lf_nf4_lora_linear(ctypes.c_void_p(16), 1, 64, ctypes.byref(w), None, None, ctypes.c_void_p(16), 64, None, 0, 0, None))
