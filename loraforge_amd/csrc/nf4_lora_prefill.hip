@@ -453,14 +453,12 @@ __device__ __forceinline__ void wait_z(const PrefillParams& p, int mt, uint32_t 
   __syncthreads();
 }
 
-// 16 bytes of z rows read with device-scope loads.
-__device__ __forceinline__ uint4 load_z16(const uint16_t* src) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(src);
-  uint4 v;
-  v.x = __hip_atomic_load(w + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.y = __hip_atomic_load(w + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.z = __hip_atomic_load(w + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.w = __hip_atomic_load(w + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// 16 bytes of z rows in one device-scope (sc1) load, coherent past this
+// XCD's L2 like the agent-scope atomics; one request instead of four.
+// Untracked: the caller waits (vmcnt) and ties the value before any use.
+__device__ __forceinline__ u32x4 load_z16(const uint16_t* src) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(src) : "memory");
   return v;
 }
 
@@ -693,13 +691,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
     const int nd = list[kMaxList];
     const int zw = p.slices * kZSlice;
     constexpr int kZq = kBM * 8 / kThreads;  // 16-byte z units per thread and slice
-    uint4 zr[kZq];
+    u32x4 zr[kZq];
+    // Every lane loads (rows past M read row M - 1, base-only rows are
+    // zeroed after the wait): no branch around the untracked loads.
     auto load_zs = [&](int s) {
 #pragma unroll
       for (int q = 0; q < kZq; ++q) {
-        const int row = (tid >> 3) + (kThreads / 8) * q;
-        zr[q] = make_uint4(0, 0, 0, 0);
-        if (tslot[row] >= 0) zr[q] = load_z16(p.zpad + int64_t(m0 + row) * zw + s * kZSlice + (tid & 7) * 8);
+        const int row = min(m0 + (tid >> 3) + (kThreads / 8) * q, p.m - 1);
+        zr[q] = load_z16(p.zpad + int64_t(row) * zw + s * kZSlice + (tid & 7) * 8);
       }
     };
     // B fragments of slot d as the MFMA's A operand: feature wn0 + 16j + c,
@@ -735,8 +734,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
         __syncthreads();  // the previous slice's readers of zs are done
         load_zs(s);
       }
+      wait_vm<0>();  // the z loads (and anything requested after them)
 #pragma unroll
-      for (int q = 0; q < kZq; ++q) zs[swz((tid >> 3) + (kThreads / 8) * q, tid & 7)] = zr[q];
+      for (int q = 0; q < kZq; ++q) tie(zr[q]);
+#pragma unroll
+      for (int q = 0; q < kZq; ++q) {
+        const int row = (tid >> 3) + (kThreads / 8) * q;
+        zs[swz(row, tid & 7)] = tslot[row] >= 0 ? make_uint4(zr[q].x, zr[q].y, zr[q].z, zr[q].w) : make_uint4(0, 0, 0, 0);
+      }
       __syncthreads();
       if (hi <= wn0 || lo >= wn0 + 48) continue;  // this wave's 48 columns miss the slice
       const bool inside = lo <= wn0 && wn0 + 48 <= hi;
