@@ -18,6 +18,9 @@ constexpr int kNf4Block = 64;
 // reset between calls). No other kernel writes it, so decode and prefill
 // calls can share one workspace.
 constexpr int64_t kWorkspaceHeader = 131072;
+// The prefill's z flags follow the header at a fixed place: 4096 flags, one
+// per 256-token tile.
+constexpr int64_t kFlagRegion = 16384;
 
 // Codebook lookup by a byte offset (nibble * 4) into a 16-entry fp32 table in
 // LDS. All lanes read at most 16 distinct words, so the read is bank-conflict

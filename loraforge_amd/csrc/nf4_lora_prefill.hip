@@ -850,12 +850,14 @@ namespace {
 int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 }  // namespace
 
-// Workspace: the control header (call epoch), the z rows (m x slices x 64
-// bf16), room for the fp32 block scales of a double-quant weight, then one
-// z flag per 256-token tile.
+// Workspace: the control header (call epoch), one z flag per 256-token tile
+// at a fixed place (so a flag word only ever holds tags, whatever the shapes
+// of earlier calls on the workspace), the z rows (m x slices x 64 bf16), then
+// room for the fp32 block scales of a double-quant weight.
+constexpr int64_t kMaxTiles = kFlagRegion / 4;
+
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int) {
-  return kWorkspaceHeader + align256(m * slices * kZSlice * 2) + align256(n * (k / kNf4Block) * 4) +
-         align256((m + wide::kBM - 1) / wide::kBM * 4) + 256;
+  return kWorkspaceHeader + kFlagRegion + align256(m * slices * kZSlice * 2) + align256(n * (k / kNf4Block) * 4);
 }
 
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
@@ -867,6 +869,8 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   LF_REQUIRE(!(lora || dq) || (workspace && workspace_bytes >= need && aligned16(workspace)),
              "workspace too small: need %lld bytes", (long long)need);
   LF_REQUIRE((m - 1) * x_stride * 2 + w->k * 2 < (int64_t(1) << 32), "x spans 4 GiB or more");
+  LF_REQUIRE((m + wide::kBM - 1) / wide::kBM <= kMaxTiles, "prefill handles at most %lld tokens per call",
+             (long long)(kMaxTiles * wide::kBM));
   auto s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   const float* scales = w->scales;
@@ -874,7 +878,8 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     // The GEMM streams fp32 block scales: rebuild them from the nested state
     // (the same reconstruction as the dequantisation kernel) after the z rows.
     const int64_t nblocks = w->n * (w->k / kNf4Block);
-    float* rebuilt = reinterpret_cast<float*>(ws + kWorkspaceHeader + align256(m * slices * kZSlice * 2));
+    float* rebuilt =
+        reinterpret_cast<float*>(ws + kWorkspaceHeader + kFlagRegion + align256(m * slices * kZSlice * 2));
     const int rc = lf_nf4_prepare_scales_dq(w->absmax_q, w->absmax2, w->code2, w->offset, w->dq_block, rebuilt,
                                             nblocks, stream);
     if (rc != kOk) return rc;
@@ -906,9 +911,8 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.lscales = lora->scales;
     p.token_slots = lora->token_slots;
     p.slice_offsets = lora->slice_offsets;
-    p.zpad = reinterpret_cast<uint16_t*>(ws + kWorkspaceHeader);  // after the decode header
-    p.zflags = reinterpret_cast<uint32_t*>(ws + kWorkspaceHeader + align256(m * slices * kZSlice * 2) +
-                                           align256(w->n * (w->k / kNf4Block) * 4));
+    p.zflags = reinterpret_cast<uint32_t*>(ws + kWorkspaceHeader);  // after the decode header
+    p.zpad = reinterpret_cast<uint16_t*>(ws + kWorkspaceHeader + kFlagRegion);
     p.ce = call_epoch_of(ws);
     p.status = reinterpret_cast<int*>(ws + kStatusOffset);
   }

@@ -28,6 +28,7 @@ from ._checks import distinct_output, require_arch, tensor, vector
 
 _WS_LOCK = threading.Lock()
 _WORKSPACES: dict = {}
+_RETIRED: list = []  # replaced workspaces a captured graph may still address
 
 
 @dataclass
@@ -98,6 +99,13 @@ def workspace_bytes(m: int, n: int, k: int, *, num_slices: int = 1, max_rank: in
 
 
 def _workspace(device, stream: int, size: int):
+    """The cached workspace of (device, stream), grown to ``size`` bytes.
+
+    A HIP graph captured earlier keeps the raw address of the buffer it was
+    captured with and writes its z rows, flags and call epoch there on every
+    replay, so a replaced buffer is never released: it moves to ``_RETIRED``
+    and stays allocated until the process ends.
+    """
     import torch
 
     key = (device.index, stream)
@@ -106,6 +114,8 @@ def _workspace(device, stream: int, size: int):
         if ws is None or ws.numel() < size:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError("warm nf4_lora_linear on this stream before graph capture")
+            if ws is not None:
+                _RETIRED.append(ws)
             ws = torch.zeros(max(size, 1 << 20), dtype=torch.uint8, device=device)
             _WORKSPACES[key] = ws
         return ws
@@ -124,19 +134,42 @@ def _kernel_takes_nested(m: int, exact: bool) -> bool:
     return m > 64 and exact
 
 
-def _prepared_scales(state):
-    """fp32 scales of a nested state, rebuilt once and kept on the state."""
+def _version(tensor):
+    try:
+        return tensor._version
+    except RuntimeError:  # tensors made under inference_mode carry no version counter
+        return None
+
+
+def scale_key(qweight, state):
+    """Version key of a state's prepared scales.
+
+    Mirrors ``integrations/_sglang_nf4_linear.py:44-57``: the state's identity
+    plus the address and version counter of the packed weight, the absmax,
+    the codebook and, for a nested state, the second-level absmax/code and
+    the offset. Contents changed outside PyTorch's versioned updates are not
+    seen (as in the reference).
+    """
+    tensors = [qweight, state.absmax, state.code]
+    if state.nested:
+        tensors += [state.state2.absmax, state.state2.code, state.offset]
+    return (id(state), tuple((t.data_ptr(), _version(t)) for t in tensors))
+
+
+def _prepared_scales(qweight, state):
+    """fp32 scales of a nested state, rebuilt whenever its version key changes."""
     from loraforge_amd.ops.nf4 import prepare_scales
 
+    key = scale_key(qweight, state)
     cached = getattr(state, "_lf_prepared_scales", None)
-    if cached is None:
+    if cached is None or cached[0] != key:
         import torch
 
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("warm nf4_lora_linear with this weight before graph capture")
-        cached = prepare_scales(state)
+        cached = (key, prepare_scales(state))
         state._lf_prepared_scales = cached
-    return cached
+    return cached[1]
 
 
 def _weight_struct(qweight, state, scales, n, k, device, m=0, exact=False):
@@ -154,7 +187,7 @@ def _weight_struct(qweight, state, scales, n, k, device, m=0, exact=False):
     if scales is None and not state.nested:
         scales = state.absmax
     if scales is None and not _kernel_takes_nested(m, exact):
-        scales = _prepared_scales(state)
+        scales = _prepared_scales(qweight, state)
     if scales is not None:
         vector(scales.reshape(-1), "scales", torch.float32, device, n * k // 64)
         w.scales = scales.data_ptr()

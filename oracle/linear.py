@@ -20,7 +20,7 @@ The SwiGLU step (``benchmarks/qwen35_decode_silu.py:50-61``,
 ``h = bf16(bf16(silu(gate)) * up)`` on the LoRA-updated bf16 gate/up values.
 
 Dot products use float64 and round through fp32 to bf16 (reference test
-convention). Pinning: tests/test_oracle_linear.py checks these functions
+convention). Pinning: tests/test_oracle_rows.py checks these functions
 against the already pinned ``oracle.rows`` operators (shrink + expand with
 one-token segments must equal the per-token chain), against ``torch`` CPU
 ``F.linear`` on the dequantised weight, and a brute-force scalar loop.

@@ -122,6 +122,45 @@ def lora_tables(rng, k, n, ranks, slices=1, bounds=None, alpha_over_r=2.0, std=0
     )
 
 
+def torch_quantized_state(n, k, *, double_quant=False, seed=0, w_std=0.02) -> dict:
+    """NF4 state dict of a seeded ``N(0, w_std)`` bf16 weight, quantised with PyTorch on the CPU.
+
+    Input generation only (the full-size configs hold up to 100M weights,
+    which the numpy quantiser takes tens of seconds for): the packed bytes and
+    scales it returns are what the oracle dequantises, so parity does not
+    depend on how they were chosen.
+    """
+    import torch
+
+    from loraforge_amd.ops.nf4 import quantize_nf4
+
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n, k, generator=g) * w_std).bfloat16()
+    q, st = quantize_nf4(w, compress_statistics=double_quant)
+    state = {
+        "qweight": q.reshape(-1).numpy().copy(),
+        "shape": (n, k),
+        "blocksize": 64,
+        "code": st.code.numpy().copy(),
+    }
+    if double_quant:
+        absmax_q = st.absmax.numpy().copy()
+        absmax2 = st.state2.absmax.numpy().copy()
+        code2 = st.state2.code.numpy().copy()
+        offset = np.float32(st.offset.item())
+        state.update(
+            absmax_q=absmax_q,
+            absmax2=absmax2,
+            code2=code2,
+            offset=offset,
+            dq_block=256,
+            scales=onf4.dq_scales(absmax_q, absmax2, code2, offset, dq_block=256),
+        )
+    else:
+        state.update(absmax=st.absmax.numpy().copy(), scales=st.absmax.numpy().copy())
+    return state
+
+
 def fused_case(
     m,
     n,
@@ -136,11 +175,13 @@ def fused_case(
     seed=731,
     token_slots=None,
     w_std=0.02,
+    state=None,
 ):
     rng = np.random.default_rng(seed)
     x = bf16(rng.standard_normal((m, k)))
-    w = onf4.bf16_to_f32(bf16(rng.standard_normal((n, k)) * w_std))
-    state = onf4.quantize(w, double_quant=double_quant)
+    if state is None:
+        w = onf4.bf16_to_f32(bf16(rng.standard_normal((n, k)) * w_std))
+        state = onf4.quantize(w, double_quant=double_quant)
     lora = lora_tables(rng, k, n, list(ranks), slices=slices, bounds=bounds)
     if token_slots is None:
         token_slots = rng.integers(0, len(ranks), m).astype(np.int32)
@@ -154,7 +195,9 @@ def fused_expected(case, rows=None):
     from oracle import linear
 
     st = case["state"]
-    w_bits = onf4.dequantize(st["qweight"], st["scales"], st["shape"])
+    w_bits = case.get("w_bits")
+    if w_bits is None:
+        w_bits = onf4.dequantize(st["qweight"], st["scales"], st["shape"])
     y = linear.nf4_linear(case["x"], w_bits, case["bias"], rows=rows)
     lora = case["lora"]
     return linear.lora_apply(
@@ -172,3 +215,54 @@ def fused_expected(case, rows=None):
         n_total=case["n"],
         columns=rows,
     )
+
+
+def segments_of(routes, max_rows=16):
+    """Group tokens by slot into segments of at most ``max_rows`` tokens (the
+    reference row_expand's segment contract, ``ops/lora_rows.py:112-239``).
+    Returns (segment_indptr, segment_slots, token_indices); base-only tokens
+    are left out."""
+    routes = np.asarray(routes)
+    indptr, seg_slots, order = [0], [], []
+    for g in sorted(set(routes.tolist()) - {-1}):
+        tokens = np.nonzero(routes == g)[0].tolist()
+        for i in range(0, len(tokens), max_rows):
+            chunk = tokens[i : i + max_rows]
+            order += chunk
+            seg_slots.append(g)
+            indptr.append(indptr[-1] + len(chunk))
+    return np.array(indptr, np.int32), np.array(seg_slots, np.int32), np.array(order, np.int32)
+
+
+def c2_case(seed=733, tokens=64, k=4096, n=4096, adapters=32, rank=16, null_frac=0.1, scale=2.0):
+    """BASELINE c2: BF16 multi-LoRA shrink/expand with no quantised base.
+
+    x bf16 [64, 4096] ~N(0,1); A [32, 16, 4096] and compact B [32][4096, 16]
+    ~N(0, 0.02); per-token slot uniform in [0, 32) with 10 % set to -1;
+    y (the base output) bf16 ~N(0, 1); ``y += 2.0 * B[idx] (A[idx] x)``.
+    """
+    rng = np.random.default_rng(seed)
+    x = bf16(rng.standard_normal((tokens, k)))
+    a = bf16(rng.standard_normal((adapters, rank, k)) * 0.02)
+    b = bf16(rng.standard_normal((adapters, n, rank)) * 0.02)
+    y = bf16(rng.standard_normal((tokens, n)))
+    routes = rng.integers(0, adapters, tokens).astype(np.int32)
+    routes[rng.random(tokens) < null_frac] = -1
+    indptr, seg_slots, order = segments_of(routes)
+    meta = dict(
+        b_offsets=np.arange(adapters, dtype=np.int64) * (n * rank),
+        b_strides=np.full(adapters, rank, np.int32),
+        ranks=np.full(adapters, rank, np.int32),
+        scales=np.full(adapters, scale, np.float32),
+        segment_indptr=indptr,
+        segment_slots=seg_slots,
+        token_indices=order,
+        slice_offsets=np.array([0, n], np.int32),
+        segment_count=np.array([len(seg_slots)], np.int32),
+    )
+    return dict(x=x, a=a, b=b.reshape(-1), y=y, z=np.zeros((tokens, rank), np.uint16), routes=routes, meta=meta)
+
+
+def zipf_routes(rng, m, adapters, s=1.1):
+    p = 1.0 / np.arange(1, adapters + 1) ** s
+    return rng.choice(adapters, size=m, p=p / p.sum()).astype(np.int32)

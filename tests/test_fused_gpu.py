@@ -340,3 +340,71 @@ def test_empty_batch_and_smallest_shapes(device):
     y = nf4_lora_linear(x, q, st, lora=lora)
     torch.cuda.synchronize()
     close(bits(y), _cases.fused_expected(big))
+
+
+def test_workspace_grown_after_capture_keeps_the_captured_buffer(device):
+    """A larger eager call on a stream after a capture replaces the cached workspace; the
+    graph keeps writing into the buffer it captured, which must stay allocated."""
+    from loraforge_amd.ops import fused
+
+    dec = _cases.fused_case(8, 1024, 1024, ranks=(16,) * 4, seed=61)
+    x, q, st, lora, _ = to_device(dec, device)
+    expect = _cases.fused_expected(dec)
+    big = _cases.fused_case(96, 4096, 4096, ranks=(16, 8), double_quant=True, seed=62)
+    xb, qb, sb, lb, _ = to_device(big, device)
+    out = torch.empty(8, 1024, dtype=torch.bfloat16, device=device)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        nf4_lora_linear(x, q, st, lora=lora, out=out)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            nf4_lora_linear(x, q, st, lora=lora, out=out)
+        captured = fused._WORKSPACES[(device.index, stream.cuda_stream)]
+        retired = len(fused._RETIRED)
+        # exact=True hands the nested state to the prefill launch, whose workspace then holds
+        # the rebuilt scales: more than the buffer the capture used.
+        yb = nf4_lora_linear(xb, qb, sb, lora=lb, exact=True)
+    torch.cuda.synchronize()
+    assert fused._WORKSPACES[(device.index, stream.cuda_stream)].data_ptr() != captured.data_ptr()
+    assert len(fused._RETIRED) == retired + 1 and fused._RETIRED[-1].data_ptr() == captured.data_ptr()
+    ref_big = yb.clone()
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+            yb2 = nf4_lora_linear(xb, qb, sb, lora=lb, exact=True)
+        torch.cuda.synchronize()
+        close(bits(out), expect)
+        assert torch.equal(yb2, ref_big)
+
+
+def test_prepared_scales_follow_in_place_weight_updates(device):
+    """The cached fp32 scales of a double-quant state are keyed on the tensors' versions
+    (reference integrations/_sglang_nf4_linear.py:44-57): an in-place reload is seen."""
+    first = _cases.fused_case(8, 512, 1024, ranks=(16,) * 4, double_quant=True, seed=71)
+    second = _cases.fused_case(8, 512, 1024, ranks=(16,) * 4, double_quant=True, seed=71, w_std=0.05)
+    x, q, st, lora, _ = to_device(first, device)
+    y1 = nf4_lora_linear(x, q, st, lora=lora)
+    torch.cuda.synchronize()
+    close(bits(y1), _cases.fused_expected(first))
+    s2 = second["state"]
+    q.copy_(torch.from_numpy(s2["qweight"]))
+    st.absmax.copy_(torch.from_numpy(s2["absmax_q"]))
+    st.state2.absmax.copy_(torch.from_numpy(s2["absmax2"]))
+    st.offset.copy_(torch.tensor(s2["offset"], dtype=torch.float32))
+    y2 = nf4_lora_linear(x, q, st, lora=lora)
+    torch.cuda.synchronize()
+    close(bits(y2), _cases.fused_expected(second))
+    # Only the absmax codes change: the key still moves and the output follows.
+    st.absmax.copy_(torch.from_numpy(first["state"]["absmax_q"]))
+    y3 = nf4_lora_linear(x, q, st, lora=lora)
+    torch.cuda.synchronize()
+    mixed = dict(second, state=dict(second["state"], absmax_q=first["state"]["absmax_q"]))
+    mixed["state"]["scales"] = _dq_scales(mixed["state"])
+    close(bits(y3), _cases.fused_expected(mixed))
+
+
+def _dq_scales(st):
+    return onf4.dq_scales(st["absmax_q"], st["absmax2"], st["code2"], st["offset"], dq_block=256)
