@@ -149,6 +149,22 @@ int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_
                        const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                        void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
 
+/* Allocation-free variant of lf_nf4_lora_linear. It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Arguments and results are those of lf_nf4_lora_linear; the
+ * workspace is a library-owned device array of LF_NOALLOC_SCRATCH_BYTES per
+ * device (held until the process ends), and problems whose
+ * lf_nf4_lora_workspace_size exceeds it are rejected with LF_EINVAL. The
+ * first call on a device clears the array on its stream and must not be
+ * captured; later calls may be. It calls no allocator. Every call on a
+ * device shares that device's array: calls that overlap in time on one GPU
+ * race. */
+#define LF_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
+int lf_nf4_lora_linear_noalloc(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* weight,
+                               const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
+                               int32_t flags, void* stream);
+
 /* Reads the workspace status word written by the last call (0 = ok); for
  * tests and diagnostics only (synchronises the stream). */
 int lf_nf4_lora_status(const void* workspace, void* stream, int32_t* status);

@@ -19,6 +19,7 @@ LF_OK = 0
 LF_EINVAL = 1
 LF_EHIP = 2
 LF_EXACT_WEIGHTS = 1
+NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024
 ABI_VERSION = 1
 
 _lock = threading.Lock()
@@ -94,6 +95,21 @@ _PROTOTYPES = {
             ctypes.POINTER(Lora),
             c_void_p,
             c_int64,
+            c_void_p,
+            c_int64,
+            c_int32,
+            c_void_p,
+        ],
+    ),
+    "lf_nf4_lora_linear_noalloc": (
+        ctypes.c_int,
+        [
+            c_void_p,
+            c_int64,
+            c_int64,
+            ctypes.POINTER(NF4Weight),
+            c_void_p,
+            ctypes.POINTER(Lora),
             c_void_p,
             c_int64,
             c_int32,
