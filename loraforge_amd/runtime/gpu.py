@@ -1,69 +1,93 @@
-"""Compact GPU residency with event-ordered copies and scoped stream leases.
+"""GPU adapter residency: one packed device image per adapter, leases on streams.
 
-Mirror of ``src/loraforge/runtime/gpu.py`` (``GPUAdapterSlots`` :25-186):
-``load`` validates on the CPU, stages pinned copies and enqueues H2D copies on
-the current stream of the pool device followed by a ready event; ``borrow``
-makes the consumer's current stream wait on that event and records the stream
-on every factor, so allocator reuse stays ordered after lease exit. Active
-leases block replacement and eviction. Graph capture is rejected.
+Reference interface: ``src/loraforge/runtime/gpu.py`` (``GPUAdapterSlots``
+:25-186, constructor, ``load``, ``borrow``, ``evict``, ``collect``,
+``tensor_bytes``); the behaviour its tests pin
+(``tests/test_runtime_gpu.py:45-140``) is kept: a load is ordered before the
+consumers of the borrowing stream, active leases block reload and eviction,
+handles go stale, graph capture is refused and the caller's current device is
+left alone.
 
-Each load allocates new storage, so factor addresses change across loads; the
-fixed-address table the fused kernels read is ``runtime.table.AdapterTable``,
-fed from ``borrow`` leases.
+How residency works here:
+
+* ``load`` reads and validates the adapter on the CPU, packs all of its
+  factors into one pinned host buffer (``slots.pack``), and enqueues ONE
+  host->device copy into ONE device buffer on the pool device's current
+  stream, followed by a ready event. The resident modules are views of that
+  buffer.
+* ``borrow`` makes the caller's current stream wait for the ready event and,
+  when the lease ends, records a "last use" event on that stream.
+* A replaced or evicted image is retired, not freed: it stays referenced
+  until its ready event and every last-use event have completed (checked on
+  each pool call and by ``collect``), so device memory is never handed back
+  to the allocator while a queued consumer may still read it. When the pool
+  itself goes away, its finalizer waits for those events.
+
+Factor addresses change from load to load; the fixed-address table that the
+fused kernels and captured graphs read is ``runtime.table.AdapterTable``,
+filled from ``borrow`` leases.
 """
 
 from __future__ import annotations
 
+import weakref
 from contextlib import contextmanager
-from dataclasses import dataclass
-from threading import RLock
-from uuid import uuid4
+from dataclasses import dataclass, field
 
-from ..adapters import AdapterModule, load_peft_adapter
-from .slots import AdapterSlots, SlotHandle, module_bytes
+from ..adapters import load_peft_adapter
+from .slots import Packed, SlotBook, SlotHandle, pack, repack
 
 
 @dataclass
-class _Resident:
-    modules: tuple
-    staging: tuple
+class _Image:
+    """One resident adapter: device buffer + module views, its pinned staging and events."""
+
+    device: Packed
+    staging: Packed | None
     ready: object
-    readers: int = 0
+    leases: int = 0
+    uses: list = field(default_factory=list)
+
+    @property
+    def payload(self) -> int:
+        return self.device.payload
+
+    @property
+    def modules(self) -> tuple:
+        return self.device.modules
+
+    def settle(self) -> bool:
+        """Drop what has completed; True once nothing queued can still touch the image."""
+        if not self.ready.query():
+            return False
+        self.staging = None
+        self.uses = [e for e in self.uses if not e.query()]
+        return not self.uses and self.leases == 0
+
+
+def _wait_all(*groups) -> None:
+    for images in groups:
+        for image in list(images):
+            image.ready.synchronize()
+            for event in image.uses:
+                event.synchronize()
 
 
 class GPUAdapterSlots:
-    """Explicit GPU slots; use factors only inside ``borrow()`` on its current stream."""
+    """Explicit GPU slots; use the factors only inside ``borrow()``, on its current stream."""
 
     def __init__(self, capacity: int, *, device: str, max_tensor_bytes: int | None = None):
         import torch
 
-        AdapterSlots(capacity, max_tensor_bytes=max_tensor_bytes)  # shared argument validation
+        self._book = SlotBook(capacity, max_tensor_bytes)
         selected = torch.device(device)
         if selected.type != "cuda" or selected.index is None:
-            raise ValueError("device must explicitly select a CUDA/ROCm GPU index")
-        with torch.cuda.device(selected):
-            if torch.cuda.is_current_stream_capturing():
-                raise RuntimeError("GPU slots do not support graph capture")
+            raise ValueError("device must explicitly select a GPU index, e.g. 'cuda:0'")
         self.device = selected
-        self._capacity = capacity
-        self._limit = max_tensor_bytes
-        self._id = uuid4().hex
-        self._lock = RLock()
-        self._generations = [0] * capacity
-        self._entries: dict[int, _Resident] = {}
-        self._pending: list[_Resident] = []
-
-    def _slot(self, slot) -> None:
-        if type(slot) is not int or not 0 <= slot < self._capacity:
-            raise ValueError("slot outside pool capacity")
-
-    def _entry(self, handle) -> _Resident:
-        if not isinstance(handle, SlotHandle) or handle.pool != self._id:
-            raise ValueError("handle belongs to a different pool")
-        self._slot(handle.slot)
-        if handle.generation != self._generations[handle.slot] or handle.slot not in self._entries:
-            raise ValueError("stale or evicted slot handle")
-        return self._entries[handle.slot]
+        self._stream()  # refuses construction under capture
+        self._retired: list = []
+        finalizer = weakref.finalize(self, _wait_all, self._retired, self._book.occupant.values())
+        finalizer.atexit = False  # at interpreter exit the process releases the device anyway
 
     def _stream(self):
         import torch
@@ -74,98 +98,86 @@ class GPUAdapterSlots:
             return torch.cuda.current_stream(self.device)
 
     def _reap(self) -> None:
-        self._pending = [e for e in self._pending if not e.ready.query()]
-        for entry in self._entries.values():
-            if entry.staging and entry.ready.query():
-                entry.staging = ()
+        for image in self._book.occupant.values():
+            image.settle()
+        self._retired[:] = [image for image in self._retired if not image.settle()]
+
+    def _retire(self, image: _Image) -> None:
+        if not image.settle():
+            self._retired.append(image)
 
     @property
     def tensor_bytes(self) -> int:
-        """Committed factor payload bytes, excluding staging and retired allocations."""
-        with self._lock:
-            return sum(module_bytes(e.modules) for e in self._entries.values())
+        """Factor payload bytes resident on the device (staging and retired images excluded)."""
+        with self._book.lock:
+            return self._book.payload()
 
     def load(self, source, slot: int) -> SlotHandle:
-        """Validate on CPU, stage pinned copies, enqueue H2D on the pool stream.
+        """Validate on the CPU, then one pinned host->device copy on the current stream.
 
-        Failure preserves the previous occupant and generation.
+        On failure the slot keeps its occupant, handle and budget.
         """
         import torch
 
-        with self._lock:
-            self._slot(slot)
+        book = self._book
+        with book.lock:
+            book.check_slot(slot)
             stream = self._stream()
             self._reap()
-            old = self._entries.get(slot)
-            if old is not None and old.readers:
+            current = book.occupant.get(slot)
+            if current is not None and current.leases:
                 raise RuntimeError("slot has active leases")
-            adapter = load_peft_adapter(source)
-            size = module_bytes(adapter.modules)
-            resident = self.tensor_bytes - (module_bytes(old.modules) if old else 0)
-            if self._limit is not None and resident + size > self._limit:
-                raise ValueError("resident tensor byte limit exceeded")
-            staging, modules = [], []
-            try:
-                with torch.cuda.device(self.device), torch.cuda.stream(stream):
-                    for module in adapter.modules:
-                        host = AdapterModule(
-                            module.name, module.a.pin_memory(), module.b.pin_memory(), module.alpha, module.use_rslora
-                        )
-                        staging.append(host)
-                        modules.append(
-                            AdapterModule(
-                                host.name,
-                                host.a.to(self.device, non_blocking=True),
-                                host.b.to(self.device, non_blocking=True),
-                                host.alpha,
-                                host.use_rslora,
-                            )
-                        )
+            host = pack(load_peft_adapter(source).modules, pin=True)
+            book.admit(slot, host.payload)
+            with torch.cuda.device(self.device), torch.cuda.stream(stream):
+                try:
+                    buffer = torch.empty_like(host.buffer, device=self.device)
+                    buffer.copy_(host.buffer, non_blocking=True)
                     ready = torch.cuda.Event()
                     ready.record(stream)
-            except BaseException:
-                stream.synchronize()  # keep partial pinned buffers alive until copies end
-                raise
-            entry = _Resident(tuple(modules), tuple(staging), ready)
-            if old is not None and old.staging:
-                self._pending.append(old)
-            self._entries[slot] = entry
-            self._generations[slot] += 1
-            return SlotHandle(self._id, slot, self._generations[slot])
+                except BaseException:
+                    stream.synchronize()  # the pinned source must outlive a copy already queued
+                    raise
+            image = _Image(repack(host, buffer), host, ready)
+            handle, previous = book.install(slot, image)
+            if previous is not None:
+                self._retire(previous)
+            return handle
 
     @contextmanager
     def borrow(self, handle: SlotHandle):
-        """Lease read-only factors for work enqueued on the current pool-device stream."""
-        with self._lock:
+        """Lease the modules of ``handle`` for work enqueued on the current stream."""
+        import torch
+
+        book = self._book
+        with book.lock:
             stream = self._stream()
             self._reap()
-            entry = self._entry(handle)
-            stream.wait_event(entry.ready)
-            for module in entry.modules:
-                module.a.record_stream(stream)
-                module.b.record_stream(stream)
-            entry.readers += 1
+            image = book.entry(handle)
+            stream.wait_event(image.ready)
+            image.leases += 1
         try:
-            yield entry.modules
+            yield image.modules
         finally:
-            with self._lock:
-                entry.readers -= 1
+            with book.lock:
+                with torch.cuda.device(self.device):
+                    done = torch.cuda.Event()
+                    done.record(stream)
+                image.uses.append(done)
+                image.leases -= 1
 
     def evict(self, handle: SlotHandle) -> None:
-        """Invalidate residency; allocator stream tracking protects queued consumers."""
-        with self._lock:
+        """End residency; the image is released once queued consumers are done with it."""
+        book = self._book
+        with book.lock:
             self._stream()
             self._reap()
-            entry = self._entry(handle)
-            if entry.readers:
+            if book.entry(handle).leases:
                 raise RuntimeError("slot has active leases")
-            if entry.staging:
-                self._pending.append(entry)
-            del self._entries[handle.slot]
-            self._generations[handle.slot] += 1
+            self._retire(book.remove(handle))
 
     def collect(self) -> None:
-        """Release completed pinned staging without waiting for GPU completion."""
-        with self._lock:
+        """Release staging buffers and retired images whose work has completed (never waits)."""
+        with self._book.lock:
             self._stream()
             self._reap()

@@ -12,6 +12,7 @@ import json
 import math
 from concurrent.futures import ThreadPoolExecutor
 
+import numpy as np
 import pytest
 import torch
 from safetensors.torch import save_file
@@ -217,3 +218,239 @@ def test_adapter_table_argument_validation():
         AdapterTable(2, in_features=60, out_features=64, device="cpu")
     with pytest.raises(ValueError):
         AdapterTable(2, in_features=64, out_features=64, slice_offsets=[0, 40, 30, 64], device="cpu")
+
+
+def test_region_allocator_first_fit_merge_and_claim():
+    from loraforge_amd.runtime.table import RegionAllocator
+
+    regions = RegionAllocator(104)
+    a, b, c = regions.take(10), regions.take(3), regions.take(20)
+    assert (a, b, c) == (0, 16, 24)  # 8-element alignment
+    assert regions.take(60) is None and regions.free == 56
+    regions.give(b, 3)
+    assert regions.take(8) == 16  # first fit reuses the hole
+    regions.give(16, 8)
+    regions.give(a, 10)
+    regions.give(c, 20)
+    assert regions.free == 104 and regions.take(104) == 0  # neighbours merged back into one range
+    regions.give(0, 104)
+    regions.claim(40, 8)
+    with pytest.raises(ValueError, match="not free"):
+        regions.claim(44, 8)
+    assert regions.take(48) == 48 and regions.take(40) == 0
+
+
+def _module(name, rank, k, n, seed, alpha=8.0):
+    from loraforge_amd.adapters import AdapterModule
+
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.randn(rank, k, generator=g) * 0.1).bfloat16()
+    b = (torch.randn(n, rank, generator=g) * 0.1).bfloat16()
+    return AdapterModule(name, a, b, alpha)
+
+
+def _dense_lora(x_bits, y_bits, slots, factors, bounds):
+    """y + bf16(scale * B_s (bf16(A_s x))) per routed token, in dense float64 algebra."""
+    from oracle import nf4 as onf4
+
+    x = onf4.bf16_to_f32(x_bits).astype(np.float64)
+    out = y_bits.copy()
+    for t, g in enumerate(slots):
+        if g < 0 or g not in factors:
+            continue
+        a_parts, b_parts, scale = factors[g]
+        for s, (lo, hi) in enumerate(zip(bounds, bounds[1:])):
+            a = onf4.bf16_to_f32(a_parts[s]).astype(np.float64)
+            b = onf4.bf16_to_f32(b_parts[s]).astype(np.float64)
+            z = onf4.bf16_to_f32(onf4.f64_to_bf16_bits(a @ x[t])).astype(np.float64)
+            delta = onf4.f64_to_bf16_bits(scale * (b @ z))
+            base = onf4.bf16_to_f32(out[t, lo:hi]).astype(np.float64)
+            out[t, lo:hi] = onf4.f64_to_bf16_bits(base + onf4.bf16_to_f32(delta))
+    return out
+
+
+def _batch_apply(batch, x_bits, y_bits, n):
+    from oracle import linear
+
+    as_np = lambda t: t.cpu().numpy()  # noqa: E731
+    return linear.lora_apply(
+        x_bits,
+        y_bits,
+        a_store=as_np(batch.a_store.view(torch.int16)).view(np.uint16),
+        a_offsets=as_np(batch.a_offsets),
+        b_store=as_np(batch.b_store.view(torch.int16)).view(np.uint16),
+        b_offsets=as_np(batch.b_offsets),
+        b_strides=as_np(batch.b_strides),
+        ranks=as_np(batch.ranks),
+        scales=as_np(batch.scales),
+        token_slots=as_np(batch.token_slots),
+        slice_offsets=as_np(batch.slice_offsets),
+        n_total=n,
+    )
+
+
+def _bits(t):
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def test_adapter_table_compact_regions_and_full_store():
+    k, bounds = 32, [0, 16, 40]
+    n = bounds[-1]
+    ranks = {0: 4, 1: 3, 2: 16}
+    need = [sum(x) for x in zip(*(AdapterTable(1, in_features=k, out_features=n, slice_offsets=bounds, device="cpu").region_elements(r) for r in ranks.values()))]
+    table = AdapterTable(4, in_features=k, out_features=n, max_rank=16, slice_offsets=bounds, device="cpu", a_elements=need[0], b_elements=need[1])
+    assert table.a_store.numel() == 2 * (4 + 3 + 16) * k  # compact: no rank-16 padding per slot
+    factors = {}
+    for slot, r in ranks.items():
+        mods = [_module(f"s{s}", r, k, hi - lo, seed=10 * slot + s) for s, (lo, hi) in enumerate(zip(bounds, bounds[1:]))]
+        table.publish(slot, mods)
+        factors[slot] = ([_bits(m.a) for m in mods], [_bits(m.b) for m in mods], mods[0].scaling)
+    assert table.ranks.tolist()[:3] == [4, 3, 16] and table.b_strides.tolist()[:3] == [4, 4, 16]
+    a_off, b_off, r = table.region_of(1)
+    assert r == 3 and a_off % 8 == 0 and b_off % 8 == 0
+    assert not table.b_store[b_off : b_off + n * 4].view(n, 4)[:, 3:].any()  # B zero padded to the bucket
+
+    # The store is full: a fourth adapter is refused and nothing changes.
+    before = [t.clone() for t in (table.a_offsets, table.b_offsets, table.ranks)]
+    with pytest.raises(ValueError, match="full"):
+        table.publish(3, [_module("s0", 2, k, 16, 1), _module("s1", 2, k, 24, 2)])
+    with pytest.raises(ValueError, match="full"):
+        table.publish(1, [_module("s0", 16, k, 16, 1), _module("s1", 16, k, 24, 2)])
+    assert all(torch.equal(x, y) for x, y in zip(before, (table.a_offsets, table.b_offsets, table.ranks)))
+    assert table.region_of(1) == (a_off, b_off, 3)
+
+    # Clearing a slot frees its regions for another adapter of the same size.
+    table.clear(1)
+    assert table.region_of(1) is None and table.ranks.tolist()[1] == 0
+    mods = [_module("s0", 3, k, 16, 77), _module("s1", 3, k, 24, 78)]
+    table.publish(3, mods)
+    factors.pop(1)
+    factors[3] = ([_bits(m.a) for m in mods], [_bits(m.b) for m in mods], mods[0].scaling)
+
+    rng = np.random.default_rng(4)
+    m_tokens = 9
+    x_bits = _bits(torch.from_numpy(rng.standard_normal((m_tokens, k)).astype(np.float32)).bfloat16())
+    y_bits = _bits(torch.from_numpy(rng.standard_normal((m_tokens, n)).astype(np.float32)).bfloat16())
+    slots = np.array([0, 1, 2, 3, -1, 3, 2, 0, 1], np.int32)
+    got = _batch_apply(table.batch(torch.from_numpy(slots)), x_bits, y_bits, n)
+    want = _dense_lora(x_bits, y_bits, slots.tolist(), factors, bounds)
+    np.testing.assert_array_equal(got[slots == 1], y_bits[slots == 1])  # cleared slot: base only
+    np.testing.assert_allclose(
+        onf4_f32(got), onf4_f32(want), rtol=1e-2, atol=1e-2
+    )
+
+
+def onf4_f32(bits):
+    from oracle import nf4 as onf4
+
+    return onf4.bf16_to_f32(bits)
+
+
+def test_retained_layout_feeds_the_fused_batch():
+    """lora_batch over a loaded layout computes the LoRA of the pool's original padded factors."""
+    slots, cap, k, width = 3, 8, 16, 24
+    g = torch.Generator().manual_seed(3)
+    a = (torch.randn(slots, 2 * cap, k, generator=g) * 0.1).bfloat16()
+    b = (torch.randn(slots, width, cap, generator=g) * 0.1).bfloat16()
+    a0, b0 = a.clone(), b.clone()
+    catalog = {"p5": catalog_ranks(5, 3), "p8": catalog_ranks(8), "p0": catalog_ranks(2, layer=1)}
+    layout = RetainedLayout(a, b, "gate_up_proj", 0, catalog)
+    layout.load("p5", 0, cap)
+    layout.load("p8", 2, cap)
+    layout.load("p0", 1, cap)  # no module of this projection: rank 0, base only
+    scales = torch.tensor([2.0, 1.0, 0.5])
+    rng = np.random.default_rng(5)
+    m_tokens = 7
+    x_bits = _bits(torch.from_numpy(rng.standard_normal((m_tokens, k)).astype(np.float32)).bfloat16())
+    y_bits = _bits(torch.from_numpy(rng.standard_normal((m_tokens, width)).astype(np.float32)).bfloat16())
+    route = np.array([0, 2, 1, -1, 2, 0, 0], np.int32)
+    batch = layout.lora_batch(torch.from_numpy(route), scales)
+    assert batch.max_rank == 8 and batch.slice_offsets.tolist() == [0, 12, 24]
+    got = _batch_apply(batch, x_bits, y_bits, width)
+    factors = {}
+    for slot, r in ((0, 5), (2, 8)):
+        a_parts = [_bits(a0[slot, s * cap : s * cap + r].contiguous()) for s in range(2)]
+        b_parts = [_bits(b0[slot, s * 12 : (s + 1) * 12, :r].contiguous()) for s in range(2)]
+        factors[slot] = (a_parts, b_parts, float(scales[slot]))
+    want = _dense_lora(x_bits, y_bits, route.tolist(), factors, [0, 12, 24])
+    np.testing.assert_array_equal(got[route == 1], y_bits[route == 1])
+    np.testing.assert_allclose(onf4_f32(got), onf4_f32(want), rtol=1e-2, atol=1e-2)
+    with pytest.raises(ValueError, match="slice_offsets"):
+        layout.lora_batch(torch.from_numpy(route), scales, slice_offsets=[0, 24])
+
+
+def test_retained_layout_refuses_wide_slots_in_the_fused_batch():
+    a = torch.zeros(2, 2 * 96, 8, dtype=torch.bfloat16)
+    b = torch.zeros(2, 16, 96, dtype=torch.bfloat16)
+    layout = RetainedLayout(a, b, "gate_up_proj", 0, {"wide": catalog_ranks(96)})
+    layout.load("wide", 0, 96)
+    with pytest.raises(ValueError, match="above 64"):
+        layout.lora_batch(torch.zeros(1, dtype=torch.int32), torch.ones(2))
+
+
+def _padded_checkpoint(root, name, rank, retained=None, nonzero_tail=False):
+    directory = root / name
+    directory.mkdir()
+    (directory / "adapter_config.json").write_text(json.dumps({"peft_type": "LORA", "r": rank, "lora_alpha": 16, "target_modules": ["gate_proj", "up_proj"]}))
+    tensors, module_ranks = {}, {}
+    for i, proj in enumerate(("gate_proj", "up_proj")):
+        key = f"base_model.model.model.layers.0.mlp.{proj}"
+        keep = rank if retained is None else retained[i]
+        a = torch.zeros(rank, 8)
+        b = torch.zeros(16, rank)
+        a[:keep] = 1.0
+        b[:, :keep] = 1.0
+        if nonzero_tail:
+            b[0, -1] = 1.0
+        tensors[key + ".lora_A.weight"], tensors[key + ".lora_B.weight"] = a, b
+        module_ranks[key + ".lora_A.weight"] = keep
+    save_file(tensors, str(directory / "adapter_model.safetensors"))
+    if retained is not None:
+        (directory / "compression.json").write_text(json.dumps({"module_ranks": module_ranks}))
+    return directory
+
+
+def test_rank_catalog_reads_headers_and_retained_ranks(tmp_path):
+    from loraforge_amd.runtime import read_rank_catalog
+
+    plain = _padded_checkpoint(tmp_path, "plain", 16)
+    reduced = _padded_checkpoint(tmp_path, "reduced", 16, retained=(3, 7))
+    catalog = read_rank_catalog([plain, reduced])
+    assert effective_rank(catalog[str(plain)], "gate_up_proj", 0) == 16
+    assert effective_rank(catalog[str(reduced)], "gate_up_proj", 0) == 7
+    bad = _padded_checkpoint(tmp_path, "bad", 16, retained=(3, 7), nonzero_tail=True)
+    with pytest.raises(ValueError, match="truncates nonzero"):
+        read_rank_catalog([bad])
+    over = _padded_checkpoint(tmp_path, "over", 4, retained=(3, 4))
+    meta = json.loads((over / "compression.json").read_text())
+    meta["module_ranks"] = {key: 5 for key in meta["module_ranks"]}
+    (over / "compression.json").write_text(json.dumps(meta))
+    with pytest.raises(ValueError, match="exceeds checkpoint rank"):
+        read_rank_catalog([over])
+    with pytest.raises(ValueError, match="nonempty"):
+        read_rank_catalog([])
+
+
+def test_safetensors_reader_rejects_malformed_files(tmp_path):
+    from loraforge_amd.adapters import read_safetensors
+
+    good = write_adapter(tmp_path, "good") / "adapter_model.safetensors"
+    tensors = read_safetensors(good)
+    assert tensors["base_model.model.proj.lora_B.weight"].shape == (5, 4)
+    blob = good.read_bytes()
+    size = int.from_bytes(blob[:8], "little")
+    header = json.loads(blob[8 : 8 + size])
+    cases = {
+        "length": (10**9).to_bytes(8, "little") + blob[8:],
+        "covered": blob + b"\0" * 8,
+    }
+    wrong_dtype = dict(header)
+    key = "base_model.model.proj.lora_A.weight"
+    wrong_dtype[key] = dict(header[key], dtype="I64")
+    raw = json.dumps(wrong_dtype).encode()
+    cases["dtype"] = len(raw).to_bytes(8, "little") + raw + blob[8 + size :]
+    for match, data in cases.items():
+        path = tmp_path / f"{match}.safetensors"
+        path.write_bytes(data)
+        with pytest.raises(ValueError, match=match):
+            read_safetensors(path)
