@@ -65,13 +65,15 @@ int lf_nf4_prepare_scales_dq(const uint8_t* absmax_q, const float* absmax2, cons
  * lf_row_shrink replaces the pybind `shrink` of ops/csrc/lora_rows.cu:172-186
  * (row_shrink, ops/lora_rows.py:54-109): x [tokens, width] with row stride
  * x_stride; a [G, num_slices*capacity, width] contiguous; z [tokens,
- * num_slices*capacity] contiguous; slots int32 [tokens]; ranks int32 [G].
+ * num_slices*capacity] contiguous; slots int32 [tokens]; ranks int32 [G];
+ * num_adapters = G (the pybind binding reads it from a's shape).
  * num_slices 1..4 (the row_shrink API allows 3, the Fleet direct_shrink of
  * ops/rowexpand.py:34-39 / rowexpand.cu:87-97 allows 4).
  * ------------------------------------------------------------------------ */
 int lf_row_shrink(const uint16_t* x, const uint16_t* a, uint16_t* z, const int32_t* slots,
                   const int32_t* ranks, int64_t tokens, int64_t width, int64_t x_stride,
-                  int32_t num_slices, int64_t capacity, int32_t max_rank, void* stream);
+                  int64_t num_adapters, int32_t num_slices, int64_t capacity, int32_t max_rank,
+                  void* stream);
 
 /* lf_row_expand replaces the pybind `expand` of ops/csrc/lora_rows.cu:188-209
  * (row_expand, ops/lora_rows.py:115-239); arguments keep that binding's

@@ -77,7 +77,7 @@ _PROTOTYPES = {
     ),
     "lf_row_shrink": (
         ctypes.c_int,
-        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, c_void_p],
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, c_void_p],
     ),
     "lf_row_expand": (
         ctypes.c_int,

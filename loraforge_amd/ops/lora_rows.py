@@ -1,11 +1,13 @@
-"""BF16 retained-rank shrink and compact-B RowExpand on gfx950.
+"""The standalone LoRA row operators (shrink to z, expand onto y) on gfx950.
 
-Mirror of ``loraforge.ops.row_shrink`` / ``row_expand``
-(``src/loraforge/ops/lora_rows.py:51-239``): same signatures, layouts,
-metadata contract and exception messages; the kernels are the HIP ones in
-``csrc/row_ops.hip`` reached through the C ABI. Device metadata values are
-trusted inputs; structural validation never copies metadata to the CPU or
-synchronises the stream.
+Drop-in for ``loraforge.ops.row_shrink`` / ``row_expand``
+(``src/loraforge/ops/lora_rows.py:51-239``): the signatures, tensor layouts,
+structural checks and the exception types and message fragments that
+callers match on are the contract kept here. The work runs in the MFMA
+kernels of ``csrc/row_ops.hip`` through the C ABI. Metadata on the device is
+used as given: the checks below look at shapes, strides, dtypes, devices
+and alignment only, so a call never reads device memory back or waits for
+the stream.
 """
 
 from __future__ import annotations
@@ -31,13 +33,14 @@ def row_shrink(
     num_slices: int = 1,
     max_rank: int = 64,
 ) -> None:
-    """Write live packed A @ x prefixes in place, rounding FP32 sums to BF16.
+    """z rows of the routed tokens: ``output[t, s*r + k] = bf16(x[t] . a[g, s*r + k])``.
 
-    x is [tokens, width], A [slots, slices * capacity, width], output
-    [tokens, slices * capacity]. For slot rank r, slice s starts at s*r in
-    both A and output. Slots -1 and rank-zero rows are left unchanged; unused
-    output columns are also unchanged. All live ranks must be <= max_rank.
-    Input width and row stride must be multiples of eight BF16 elements.
+    ``g = slots[t]`` and ``r = ranks[g]``; tokens routed to -1 or to a rank-0
+    slot, and every column at or past ``num_slices * r``, keep their values.
+    Shapes: x [tokens, width] (width and row stride multiples of 8, 16-byte
+    aligned), a [slots, num_slices * capacity, width] contiguous, output
+    [tokens, num_slices * capacity] contiguous; every live rank is at most
+    ``max_rank``. Runs on the caller's current stream; no host sync.
     """
     import torch
 
@@ -86,6 +89,7 @@ def row_shrink(
                 x.shape[0],
                 x.shape[1],
                 x.stride(0),
+                a.shape[0],
                 num_slices,
                 a.shape[1] // num_slices,
                 max_rank,
@@ -112,17 +116,18 @@ def row_expand(
     blocks: int | None = None,
     threads: int = 256,
 ) -> None:
-    """Add compact B @ z to BF16 output, reusing B across <=16 token segments.
+    """Adds each segment's LoRA expansion to its tokens' rows of ``output``, in place.
 
-    z is [tokens, slices * capacity], with each live slice packed at s*r.
-    B is flat; b_offsets are element offsets and b_strides are power-of-two
-    row widths in 1..64, at least the corresponding rank. B padding is zero.
-    Each segment has one slot and at most 16 distinct token indices. Tokens
-    occur at most once across active segments. slice_offsets partition output
-    columns; segment_count is a one-element int32 device vector.
-
-    FP32 dot products are scaled, rounded to BF16, added to the BF16 base,
-    and rounded again. Rank-zero and slot -1 segments leave output unchanged.
+    A segment is at most 16 distinct tokens routed to one slot g (rank r,
+    scale ``scales[g]``); for a column n of slice s it adds
+    ``bf16(scales[g] * sum_{k<r} z[t, s*r + k] * B_g[n, k])`` to the bf16
+    value and rounds again. ``B_g`` is ``[out, b_strides[g]]`` at element
+    ``b_offsets[g]`` of the flat store ``b`` (strides are powers of two in
+    1..64, zero padded past r); ``slice_offsets`` partitions the output
+    columns and ``segment_count`` (one int32 on the device) says how many
+    segments are live, so nothing is read back to the host. Slot -1 and
+    rank-0 segments change nothing; a token may sit in one live segment only.
+    ``blocks`` / ``threads`` size the persistent grid.
     """
     import torch
 

@@ -83,6 +83,7 @@ def direct_shrink(x: Tensor, weights: Tensor, output: Tensor, routes: Tensor, ra
                 x.shape[0],
                 x.shape[1],
                 x.stride(0),
+                weights.shape[0],
                 slices,
                 weights.shape[1] // slices,
                 max_rank,
