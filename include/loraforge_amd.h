@@ -73,17 +73,35 @@ int lf_nf4_prepare_scales_dq(const uint8_t* absmax_q, const float* absmax2, cons
 int lf_row_shrink(const uint16_t* x, const uint16_t* a, uint16_t* z, const int32_t* slots,
                   const int32_t* ranks, int64_t tokens, int64_t width, int64_t x_stride,
                   int64_t num_adapters, int32_t num_slices, int64_t capacity, int32_t max_rank,
-                  void* stream);
+                  void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
+
+/* Bytes of workspace lf_row_shrink needs (0: none). Small token counts split
+ * K across workgroups and sum the fp32 partials in the workspace; it must be
+ * zero before its first use and is never reset between calls (entries carry
+ * the tag of the call that wrote them, as in lf_nf4_lora_workspace_size).
+ * Calls that share a workspace must not overlap; lf_nf4_lora_status reads
+ * its status word (1: a partial had to be recomputed by the summing
+ * workgroup after a bounded wait; the result is still exact). */
+int64_t lf_row_shrink_workspace_size(int64_t tokens, int64_t width, int64_t num_adapters,
+                                     int32_t num_slices, int32_t max_rank);
+
+/* Test hook for lf_row_shrink only: K chunks past the first publish no
+ * partials, so every summing workgroup gives up its (shortened) wait and
+ * recomputes them; the output must not change. */
+#define LF_TEST_WITHHOLD_PARTIALS 0x100
 
 /* lf_row_expand replaces the pybind `expand` of ops/csrc/lora_rows.cu:188-209
  * (row_expand, ops/lora_rows.py:115-239); arguments keep that binding's
- * order and meaning. b_strides is the reference's "buckets". */
+ * order and meaning. b_strides is the reference's "buckets". segments is the
+ * length of segment_slots (segment_indptr holds segments + 1 entries; the
+ * binding reads it from the tensor): the kernel reads a segment's bounds and
+ * slot together with the live count instead of after it. */
 int lf_row_expand(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets,
                   const int32_t* b_strides, uint16_t* y, const int32_t* segment_indptr,
                   const int32_t* segment_slots, const int32_t* token_indices, const int32_t* ranks,
                   const float* scales, const int32_t* slice_offsets, const int32_t* segment_count,
-                  int64_t tokens, int64_t out_width, int64_t y_stride, int32_t num_slices,
-                  int64_t capacity, int32_t blocks, int32_t threads, void* stream);
+                  int64_t segments, int64_t tokens, int64_t out_width, int64_t y_stride,
+                  int32_t num_slices, int64_t capacity, int32_t blocks, int32_t threads, void* stream);
 
 /* --------------------------------------------------------------------------
  * Fused NF4 base linear + per-token multi-LoRA (one launch for decode).

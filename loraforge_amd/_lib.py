@@ -19,6 +19,7 @@ LF_OK = 0
 LF_EINVAL = 1
 LF_EHIP = 2
 LF_EXACT_WEIGHTS = 1
+LF_TEST_WITHHOLD_PARTIALS = 0x100
 NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024
 ABI_VERSION = 1
 
@@ -77,11 +78,16 @@ _PROTOTYPES = {
     ),
     "lf_row_shrink": (
         ctypes.c_int,
-        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, c_void_p],
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32]
+        + [c_void_p, c_int64, c_int32, c_void_p],
+    ),
+    "lf_row_shrink_workspace_size": (
+        c_int64,
+        [c_int64, c_int64, c_int64, c_int32, c_int32],
     ),
     "lf_row_expand": (
         ctypes.c_int,
-        [c_void_p] * 12 + [c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, c_int32, c_void_p],
+        [c_void_p] * 12 + [c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, c_int32, c_void_p],
     ),
     "lf_nf4_lora_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int32, c_int32]),
     "lf_nf4_lora_linear": (

@@ -3,8 +3,9 @@
 // prefill z rows).
 //
 // Every workgroup reads the epoch word at its start; the call's tag is
-// epoch + 1. When its work is done a workgroup counts itself in (one counter
-// per blockIdx % 8, so no single address takes every atomic); the last of a
+// epoch + 1. Once it holds its tag a workgroup counts itself in (one counter
+// per blockIdx % 8, so no single address takes every atomic; it may do so
+// right away and look at the returned count only at its end); the last of a
 // group counts the group in, and the last group resets the counters and moves
 // the epoch on. Every workgroup has read the epoch before it counts in, so all
 // workgroups of a call see the same tag and no earlier call used it (tags

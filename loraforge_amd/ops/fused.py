@@ -98,8 +98,10 @@ def workspace_bytes(m: int, n: int, k: int, *, num_slices: int = 1, max_rank: in
     return int(size)
 
 
-def _workspace(device, stream: int, size: int):
+def _workspace(device, stream: int, size: int, kind: str = "fused"):
     """The cached workspace of (device, stream), grown to ``size`` bytes.
+
+    ``kind`` keeps the fused linear's and the row shrink's buffers apart.
 
     A HIP graph captured earlier keeps the raw address of the buffer it was
     captured with and writes its z rows, flags and call epoch there on every
@@ -108,12 +110,15 @@ def _workspace(device, stream: int, size: int):
     """
     import torch
 
-    key = (device.index, stream)
+    key = (device.index, stream) if kind == "fused" else (kind, device.index, stream)
     with _WS_LOCK:
         ws = _WORKSPACES.get(key)
         if ws is None or ws.numel() < size:
-            if torch.cuda.is_current_stream_capturing():
+            if torch.cuda.is_current_stream_capturing() and kind == "fused":
                 raise RuntimeError("warm nf4_lora_linear on this stream before graph capture")
+            # (A row-shrink workspace may be made under capture: it comes from the
+            # graph's pool and its zero fill is a kernel of the graph, so every
+            # replay starts from a zeroed workspace, which the tags allow.)
             if ws is not None:
                 _RETIRED.append(ws)
             ws = torch.zeros(max(size, 1 << 20), dtype=torch.uint8, device=device)

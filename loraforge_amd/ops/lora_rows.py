@@ -22,6 +22,19 @@ if TYPE_CHECKING:
     from torch import Tensor
 
 
+def _shrink_workspace(x, adapters: int, slices: int, max_rank: int) -> tuple:
+    """(pointer, bytes) of the cached workspace a shrink of ``x`` needs (none: (None, 0))."""
+    from .fused import _workspace
+
+    need = _lib.library().lf_row_shrink_workspace_size(x.shape[0], x.shape[1], adapters, slices, max_rank)
+    if need < 0:
+        raise ValueError("invalid shrink problem size")
+    if need == 0:
+        return None, 0
+    ws = _workspace(x.device, _lib.stream_of(x.device), int(need), kind="rows")
+    return ws.data_ptr(), ws.numel()
+
+
 @ExperimentalAPI(reason="BF16 retained-rank inference operator; gfx950 HIP kernel, caller-owned device metadata.")
 def row_shrink(
     x: Tensor,
@@ -93,6 +106,8 @@ def row_shrink(
                 num_slices,
                 a.shape[1] // num_slices,
                 max_rank,
+                *_shrink_workspace(x, a.shape[0], num_slices, max_rank),
+                0,
                 _lib.stream_of(x.device),
             )
         )
@@ -197,6 +212,7 @@ def row_expand(
                 scales.data_ptr(),
                 slice_offsets.data_ptr(),
                 segment_count.data_ptr(),
+                segment_slots.numel(),
                 z.shape[0],
                 output.shape[1],
                 output.stride(0),

@@ -15,6 +15,7 @@ from __future__ import annotations
 from typing import TYPE_CHECKING
 
 from .. import _lib
+from .lora_rows import _shrink_workspace
 from ._checks import distinct_output, require_arch, tensor, vector
 
 if TYPE_CHECKING:
@@ -87,6 +88,8 @@ def direct_shrink(x: Tensor, weights: Tensor, output: Tensor, routes: Tensor, ra
                 slices,
                 weights.shape[1] // slices,
                 max_rank,
+                *_shrink_workspace(x, weights.shape[0], slices, max_rank),
+                0,
                 _lib.stream_of(x.device),
             )
         )
@@ -174,6 +177,7 @@ def row_expand(
                 scales.data_ptr(),
                 slice_offsets.data_ptr(),
                 segment_count.data_ptr(),
+                slots.numel(),
                 z.shape[0],
                 output.shape[1],
                 output.stride(0),

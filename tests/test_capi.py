@@ -38,9 +38,9 @@ def test_validation_errors_without_device_work():
     assert status == _lib.LF_EINVAL
     assert b"multiple of 4096" in lib.lf_last_error()
     with pytest.raises(ValueError, match="threads"):
-        _lib.check(lib.lf_row_expand(*([ctypes.c_void_p(8)] * 12), 4, 4, 4, 1, 4, 64, 64, None))
+        _lib.check(lib.lf_row_expand(*([ctypes.c_void_p(8)] * 12), 2, 4, 4, 4, 1, 4, 64, 64, None))
     with pytest.raises(ValueError, match="num_slices"):
-        _lib.check(lib.lf_row_shrink(*([ctypes.c_void_p(16)] * 5), 4, 64, 64, 2, 5, 64, 16, None))
+        _lib.check(lib.lf_row_shrink(*([ctypes.c_void_p(16)] * 5), 4, 64, 64, 2, 5, 64, 16, None, 0, 0, None))
     with pytest.raises(ValueError, match="null pointer"):
         _lib.check(lib.lf_swiglu(None, 1, 8, 16, None, 8, None))
     with pytest.raises(ValueError, match="2 \\* n"):

@@ -216,3 +216,84 @@ def test_empty_batch_and_zero_active_segments(device):
     assert torch.equal(output, before)
     row_shrink(x[:0], a, z[:0], routes[:0], meta["ranks"])
     row_expand(z[:0], b, output[:0], **meta)
+
+
+def _shrink_case(tokens, seed, adapters=32, rank=16, k=4096):
+    c = _cases.c2_case(seed=seed, tokens=tokens, k=k, n=64, adapters=adapters, rank=rank)
+    c["z"] = np.full(c["z"].shape, _cases.bf16(3.0), np.uint16)
+    return c
+
+
+@pytest.mark.parametrize("tokens", [1, 17, 64, 200, 256, 257, 700])
+def test_shrink_token_counts_across_the_k_split(tokens, device):
+    """Up to 256 tokens split K over workgroups (tagged partials, elected sum); above, one pass."""
+    c = _shrink_case(tokens, seed=900 + tokens)
+    x, a, z = t16(c["x"], device), t16(c["a"], device), t16(c["z"], device)
+    routes = torch.from_numpy(c["routes"]).to(device)
+    ranks = torch.from_numpy(c["meta"]["ranks"]).to(device)
+    for _ in range(2):  # the second call reuses the workspace with a new tag
+        row_shrink(x, a, z, routes, ranks, max_rank=16)
+        torch.cuda.synchronize()
+        zb = bits(z)
+        expected = rows.row_shrink(c["x"], c["a"], c["z"], c["routes"], c["meta"]["ranks"])
+        live = c["routes"] >= 0
+        if live.any():
+            close(zb[live], expected[live])
+        assert np.array_equal(zb[~live], c["z"][~live])
+
+
+def test_shrink_gives_up_on_withheld_partials_and_recomputes(device):
+    """Host-forced give-up: chunks past the first never publish; the summing workgroup's bounded
+    wait ends, it recomputes those chunks from x and A, flags the status word, and z is exact."""
+    import ctypes
+
+    from loraforge_amd import _lib
+
+    c = _shrink_case(64, seed=933)
+    x, a, z = t16(c["x"], device), t16(c["a"], device), t16(c["z"], device)
+    routes = torch.from_numpy(c["routes"]).to(device)
+    ranks = torch.from_numpy(c["meta"]["ranks"]).to(device)
+    lib = _lib.library()
+    need = lib.lf_row_shrink_workspace_size(64, 4096, 32, 1, 16)
+    assert need > 0  # 64 tokens split K
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    expected = rows.row_shrink(c["x"], c["a"], c["z"], c["routes"], c["meta"]["ranks"])
+    live = c["routes"] >= 0
+
+    def call(flags):
+        _lib.check(
+            lib.lf_row_shrink(
+                x.data_ptr(), a.data_ptr(), z.data_ptr(), routes.data_ptr(), ranks.data_ptr(), 64, 4096, 4096, 32, 1, 16, 16,
+                ws.data_ptr(), need, flags, _lib.stream_of(device),
+            )
+        )
+        status = ctypes.c_int32(-1)
+        _lib.check(lib.lf_nf4_lora_status(ws.data_ptr(), _lib.stream_of(device), ctypes.byref(status)))
+        return status.value
+
+    assert call(0) == 0
+    close(bits(z)[live], expected[live])
+    z.copy_(t16(c["z"], device))
+    assert call(_lib.LF_TEST_WITHHOLD_PARTIALS) == 1
+    zb = bits(z)
+    close(zb[live], expected[live])
+    assert np.array_equal(zb[~live], c["z"][~live])
+    ws[8:12].zero_()  # clear the status word; a normal call afterwards is clean again
+    z.copy_(t16(c["z"], device))
+    assert call(0) == 0
+    close(bits(z)[live], expected[live])
+
+
+def test_shrink_shapes_alternate_on_one_workspace(device):
+    """Calls of different shapes share the cached workspace: the election counters of one shape
+    land where another shape kept partials, so they must be at a place of their own."""
+    for tokens, rank, adapters in [(64, 16, 32), (40, 64, 8), (64, 16, 32), (9, 8, 100), (64, 16, 32)]:
+        c = _shrink_case(tokens, seed=tokens * rank + adapters, adapters=adapters, rank=rank)
+        x, a, z = t16(c["x"], device), t16(c["a"], device), t16(c["z"], device)
+        routes = torch.from_numpy(c["routes"]).to(device)
+        ranks = torch.from_numpy(c["meta"]["ranks"]).to(device)
+        row_shrink(x, a, z, routes, ranks, max_rank=rank)
+        torch.cuda.synchronize()
+        live = c["routes"] >= 0
+        expected = rows.row_shrink(c["x"], c["a"], c["z"], c["routes"], c["meta"]["ranks"])
+        close(bits(z)[live], expected[live])
