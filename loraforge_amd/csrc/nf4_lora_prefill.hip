@@ -7,21 +7,22 @@
 //
 // One launch (wide::gemm_kernel) on the caller's stream (a double-quant
 // weight first gets its fp32 block scales rebuilt into the workspace):
-//  - LoRA launches start with one z producer per 256-token tile: z =
-//    bf16(x A_g^T) of the tile's routed tokens, on the GEMM's own LDS
-//    pipeline and MFMA fragments, into a slice-padded workspace
-//    zpad[m][s*64 + j] (zeros past r), then the tile's flag is set to the
-//    call's tag (call_epoch.h).
+//  - LoRA launches start with zparts z producers per 256-token tile, each
+//    serving a share of the tile's distinct adapters: z = bf16(x A_g^T) of
+//    just the tokens routed to g (gathered, 16 per wave, MFMA), into a
+//    slice-padded workspace zpad[m][s*64 + j] (zeros past r), then the
+//    producer's flag is set to the call's tag (call_epoch.h).
 //  - GEMM tiles of 256 tokens x 192 output features: x streamed by direct
 //    global -> LDS copies, W decoded once per tile to the reference's exact
 //    weights bf16_rne(code * scale) into LDS, contracted on
 //    v_mfma_f32_16x16x32_bf16. LDS rows are 128 B with a 16-byte-unit XOR
 //    swizzle (unit ^ row % 8). Epilogue: round, bias; with LoRA, wait for the
-//    tile's flag (its producer has a lower block id, so it is already
-//    running), stage the tile's z rows per slice in LDS and, for every
+//    flags of the tile's producers (lower block ids, so already running), stage the tile's z rows per slice in LDS and, for every
 //    distinct slot in the tile, a second MFMA pass z x B_g^T over the 16-row
 //    blocks holding its tokens gives the delta, applied with the reference's
 //    two bf16 roundings to the rows routed to that slot.
+#include <algorithm>
+
 #include "call_epoch.h"
 #include "lds_pipeline.h"
 #include "nf4_common.h"
@@ -59,10 +60,11 @@ struct PrefillParams {
   int slices;
   uint16_t* zpad;     // [m][slices * 64]
   int y_vec;          // 2: 16-byte aligned y rows, 1: 8-byte aligned, 0: neither
-  uint32_t* zflags;   // [mtiles]: the call's tag once the tile's z rows are stored
+  uint32_t* zflags;   // [mtiles * zparts]: the call's tag once a producer's z rows are stored
   CallEpoch ce;
   int* status;  // set to 1 if a wait for z gives up (cannot happen while producers run first)
   int mtiles;
+  int zparts;   // z producers per M-tile
 };
 
 __device__ __forceinline__ int swz(int row, int unit) { return row * 8 + (unit ^ (row & 7)); }
@@ -103,13 +105,27 @@ __device__ void live_slots(const PrefillParams& p, int t0, int count, int* tslot
   __syncthreads();
 }
 
-// LoRA B row segment [kk, kk + 8) of a row of length br (zeros past br).
-__device__ __forceinline__ uint4 load_b8(const uint16_t* brow, int kk, int br) {
-  if (kk + 8 <= br) return *reinterpret_cast<const uint4*>(brow + kk);
-  uint32_t h[8];
+// Raw B values kk .. kk + 7 of one row (stride br, a power of two; kk a
+// multiple of 8) from a readable place: rows of stride >= 8 are 16-byte
+// aligned and kk is clamped into the row; a narrower row is read whole (8,
+// 4 or 2 bytes, aligned). keep_first() then keeps what belongs to B[kk..].
+__device__ __forceinline__ uint4 b_raw(const uint16_t* row, int br, int kk) {
+  if (br >= 8) return *reinterpret_cast<const uint4*>(row + min(kk, br - 8));
+  if (br == 4) {
+    const uint2 v = *reinterpret_cast<const uint2*>(row);
+    return make_uint4(v.x, v.y, 0u, 0u);
+  }
+  if (br == 2) return make_uint4(*reinterpret_cast<const uint32_t*>(row), 0u, 0u, 0u);
+  return make_uint4(row[0], 0u, 0u, 0u);
+}
+
+// The first `keep` bf16 values of v (none when keep <= 0), zeros after.
+__device__ __forceinline__ uint4 keep_first(uint4 v, int keep) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = kk + e < br ? brow[kk + e] : 0u;
-  return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+  for (int e = 0; e < 8; ++e)
+    if (e >= keep) w[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -279,157 +295,152 @@ __device__ __forceinline__ void wait_lgkm() {
   __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));  // lgkmcnt(N) only
 }
 
-// z producer of M-tile mt (the launch's workgroups below mtiles): z rows
-// bf16(x A_g^T) of every token of the tile routed to a live slot, in the
-// slice-padded layout zpad[t][s * 64 + j] (zeros for j >= r), then the tile's
-// flag is set to the call's tag. The columns of a pass are up to kBN rows of
-// the distinct slots' A factors ([slices * r, K] each, concatenated); a pass
-// streams the x tile and those rows through the GEMM's LDS layout (direct
-// copies, two-step x ring, one-step A slots) and contracts them on the same
-// MFMA fragments; each output is kept for the rows routed to its slot.
-__device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, uint32_t tag, char* xring, uint4* wdec,
-                                          int* tslot, int* list, int* colmap, int* cum) {
+// z producers: the launch's first mtiles * zparts workgroups. The tokens of
+// M-tile mt routed to live slots are sorted by slot (counting sort in LDS)
+// and cut into units of up to 16 tokens of one slot; producer (mt, q) takes
+// units q, q + zparts, ... For a unit it contracts just those tokens with the
+// slices * r rows of A_g, 64 rows (four 16-row tiles) per pass: the eight
+// waves take interleaved 32-wide k steps (v_mfma_f32_16x16x32_bf16, A rows as
+// the A operand, the tokens' x as the B operand, four steps of loads in
+// flight), the partial tiles meet in LDS in a fixed order, and
+// z = bf16(x A_g^T) is stored in the slice-padded layout zpad[t][s * 64 + j]
+// (zeros for r <= j < 64). Finally the producer sets its flag
+// zflags[mt * zparts + q] to the call's tag. Work follows the routed tokens:
+// a dense pass over the whole tile for every slot's rows would multiply the
+// LoRA FLOPs by the number of slots in the tile (Zipf routing over 128
+// adapters puts dozens in one tile).
+// A device-coherent (sc1) 2-byte store: performed at the level the
+// consumers' sc1 z loads read, so the producer needs no L2 write-back
+// (release fence) before its flag, only a wait for its stores to complete.
+__device__ __forceinline__ void store_z(uint16_t* dst, uint16_t v) {
+  asm volatile("global_store_short %0, %1, off sc1" : : "v"(dst), "v"(uint32_t(v)) : "memory");
+}
+
+constexpr int kUnit = 16;        // tokens per unit
+constexpr int kUnitRows = 64;    // A rows per pass
+constexpr int kUnitSteps = 4;    // k steps of loads in flight per wave
+
+__device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, int q, uint32_t tag, int* tslot, int* list,
+                                          int* order, int* cnt, int* ustart, float* red) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
   const int c = lane & 15;
-  const int g = lane >> 4;
+  const int kg = lane >> 4;
+  constexpr int kWaves = kThreads / 64;
   const int m0 = mt * kBM;
   const int count = min(kBM, p.m - m0);
-  const int nk = p.k / kBK;
   const int zw = p.slices * kZSlice;
+  const int steps = p.k / 32;
   live_slots(p, m0, count, tslot, list);
   const int nd = list[kMaxList];
-  // Column offsets of the distinct slots (cum[d] .. cum[d + 1]).
-  if (tid == 0) {
-    int acc = 0;
-    for (int d = 0; d < nd; ++d) {
-      cum[d] = acc;
-      acc += p.slices * p.ranks[list[d]];
-    }
-    cum[nd] = acc;
-  }
-  // Zero columns r .. 64 of every slice of the live tokens.
-  for (int i = tid; i < count * zw; i += kThreads) {
-    const int t = i / zw;
-    const int col = i - t * zw;
-    const int gt = tslot[t];
-    if (gt >= 0 && (col % kZSlice) >= p.ranks[gt]) p.zpad[int64_t(m0 + t) * zw + col] = 0;
+  // Counting sort of the tile's live tokens by distinct slot index.
+  for (int d = tid; d <= nd; d += kThreads) cnt[d] = 0;
+  __syncthreads();
+  // Every producer of the tile must cut the same units, so a token's place is
+  // fixed: its slot's first position plus the number of earlier tokens of the
+  // same slot (a broadcast scan of tslot, not an LDS atomic's arrival order).
+  int my_d = -1, my_rank = 0;
+  if (tid < count && tslot[tid] >= 0) {
+    const int gt = tslot[tid];
+    for (int d = 0; d < nd; ++d)
+      if (list[d] == gt) my_d = d;
+    for (int i = 0; i < tid; ++i) my_rank += tslot[i] == gt;
+    atomicAdd(&cnt[my_d], 1);
   }
   __syncthreads();
-  const int ncols = cum[nd];
-  const uint32_t xa0 = lds_addr(xring) + uint32_t((wm * 128 + c) * 128 + ((g ^ (c & 7)) << 4));
-  const uint32_t xa1 = lds_addr(xring) + uint32_t((wm * 128 + c) * 128 + (((4 + g) ^ (c & 7)) << 4));
-  const uint32_t wa0 = lds_addr(wdec) + uint32_t((wn * 48 + c) * 128 + ((g ^ (c & 7)) << 4));
-  const uint32_t wa1 = lds_addr(wdec) + uint32_t((wn * 48 + c) * 128 + (((4 + g) ^ (c & 7)) << 4));
-  for (int c0 = 0; c0 < ncols; c0 += kBN) {
-    // colmap[col] = (distinct slot << 16) | (slice << 8) | row within the slice, or -1.
-    if (tid < kBN) {
-      const int col = c0 + tid;
-      int e = -1;
-      if (col < ncols) {
-        int d = 0;
-        while (cum[d + 1] <= col) ++d;
-        const int rho = col - cum[d];
-        const int r = p.ranks[list[d]];
-        e = (d << 16) | ((rho / r) << 8) | (rho % r);
+  if (tid == 0) {
+    int pos = 0, units = 0;
+    for (int d = 0; d < nd; ++d) {
+      const int n = cnt[d];
+      cnt[d] = pos;       // first position of slot d's tokens in `order`
+      ustart[d] = units;  // first unit of slot d
+      pos += n;
+      units += (n + kUnit - 1) / kUnit;
+    }
+    cnt[nd] = pos;
+    ustart[nd] = units;
+  }
+  __syncthreads();
+  if (my_d >= 0) order[cnt[my_d] + my_rank] = tid;  // slot d holds positions cnt[d] .. cnt[d + 1]
+  __syncthreads();
+  // Zero the padding columns r .. 63 of every slice of the tokens this producer serves.
+  const int units = ustart[nd];
+  for (int u = q; u < units; u += p.zparts) {
+    int d = 0;
+    while (ustart[d + 1] <= u) ++d;
+    const int first = cnt[d] + (u - ustart[d]) * kUnit;
+    const int ntok = min(kUnit, cnt[d + 1] - first);
+    const int r = p.ranks[list[d]];
+    for (int i = tid; i < ntok * zw; i += kThreads) {
+      const int t = i / zw;
+      const int col = i - t * zw;
+      if ((col & (kZSlice - 1)) >= r) store_z(p.zpad + int64_t(m0 + order[first + t]) * zw + col, 0);
+    }
+  }
+  for (int u = q; u < units; u += p.zparts) {
+    int d = 0;
+    while (ustart[d + 1] <= u) ++d;
+    const int first = cnt[d] + (u - ustart[d]) * kUnit;
+    const int ntok = min(kUnit, cnt[d + 1] - first);
+    const int gd = list[d];
+    const int r = p.ranks[gd];
+    const int rows = p.slices * r;
+    const uint16_t* abase = p.a_store + p.a_offsets[gd];
+    const int tok = m0 + order[first + min(c, ntok - 1)];
+    const uint16_t* xrow = p.x + int64_t(tok) * p.x_stride + 8 * kg;
+    for (int j0 = 0; j0 < rows; j0 += kUnitRows) {
+      f32x4 acc[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) acc[jt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      const int tiles = (min(kUnitRows, rows - j0) + 15) >> 4;  // uniform
+      for (int s0 = wave; s0 < steps; s0 += kWaves * kUnitSteps) {
+        // Loads of this batch's steps first (past the end: a readable step, not contracted).
+        uint4 xb[kUnitSteps], ab[kUnitSteps][4];
+#pragma unroll
+        for (int v = 0; v < kUnitSteps; ++v) {
+          const int st = min(s0 + v * kWaves, steps - 1);
+          xb[v] = *reinterpret_cast<const uint4*>(xrow + st * 32);
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+            if (jt < tiles)
+              ab[v][jt] = *reinterpret_cast<const uint4*>(abase + int64_t(min(j0 + jt * 16 + c, rows - 1)) * p.k +
+                                                          st * 32 + 8 * kg);
+        }
+#pragma unroll
+        for (int v = 0; v < kUnitSteps; ++v)
+          if (s0 + v * kWaves < steps)
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt)
+              if (jt < tiles) acc[jt] = mfma16(as_bf16x8(ab[v][jt]), as_bf16x8(xb[v]), acc[jt]);
       }
-      colmap[tid] = e;
-    }
-    __syncthreads();
-    // This lane's three A-row copies per step: position P = (wave * 3 + q) * 64
-    // + lane -> row P / 8, slot P % 8 holding unit (P % 8) ^ (row & 7).
-    const uint16_t* asrc[3];
+      // acc[jt][e] = this wave's partial of z[token c][A row j0 + 16 jt + 4 kg + e].
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      const int pos = (wave * 3 + q) * 64 + lane;
-      const int row = pos >> 3;
-      const int u = (pos & 7) ^ (row & 7);
-      const int e = colmap[row];
-      const int d = e < 0 ? 0 : e >> 16;
-      const int rho = e < 0 ? 0 : (((e >> 8) & 0xff) * p.ranks[list[d]] + (e & 0xff));
-      asrc[q] = p.a_store + p.a_offsets[list[d]] + int64_t(rho) * p.k + u * 8;
-    }
-    auto issue_a = [&](int kt, int slot) {
+      for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-      for (int q = 0; q < 3; ++q)
-        copy16(asrc[q] + kt * kBK, reinterpret_cast<char*>(wdec) + slot * kWBytes + (wave * 3 + q) * 1024);
-    };
-    const bool busy = wn * 48 < ncols - c0;  // the wave's columns hold A rows
-    f32x4 acc[8][kJ];
+        for (int e = 0; e < 4; ++e) red[((wave * 4 + jt) * 16 + 4 * kg + e) * 17 + c] = acc[jt][e];
+      __syncthreads();
+      for (int o = tid; o < kUnitRows * kUnit; o += kThreads) {
+        const int jr = o >> 4;  // A row within the pass
+        const int t = o & 15;
+        const int j = j0 + jr;
+        if (t < ntok && j < rows) {
+          float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < kJ; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    issue_x(p, xring, m0, 0, wave, lane);
-    issue_x(p, xring + kXBytes, m0, min(1, nk - 1), wave, lane);
-    issue_a(0, 0);
-    wait_vm<0>();
-    lds_barrier();
-    for (int kt = 0; kt < nk; ++kt) {
-      // Requests: A(kt + 1), then x(kt + 2) (past the end: the last step again).
-      issue_a(min(kt + 1, nk - 1), (kt + 1) & 1);
-      issue_x(p, xring + ((kt + 2) % kXD) * kXBytes, m0, min(kt + 2, nk - 1), wave, lane);
-      if (busy) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t ax = (h ? xa1 : xa0) + uint32_t((kt % kXD) * kXBytes);
-          const uint32_t bx = (h ? wa1 : wa0) + uint32_t((kt & 1) * kWBytes);
-          u32x4 a[8], b[kJ];
-          a[0] = ldsr128<0 * 2048>(ax);
-          a[1] = ldsr128<1 * 2048>(ax);
-          a[2] = ldsr128<2 * 2048>(ax);
-          a[3] = ldsr128<3 * 2048>(ax);
-          a[4] = ldsr128<4 * 2048>(ax);
-          a[5] = ldsr128<5 * 2048>(ax);
-          a[6] = ldsr128<6 * 2048>(ax);
-          a[7] = ldsr128<7 * 2048>(ax);
-          b[0] = ldsr128<0 * 2048>(bx);
-          b[1] = ldsr128<1 * 2048>(bx);
-          b[2] = ldsr128<2 * 2048>(bx);
-          wait_lgkm<0>();
-#pragma unroll
-          for (int i = 0; i < 8; ++i) tie(a[i]);
-#pragma unroll
-          for (int j = 0; j < kJ; ++j) tie(b[j]);
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int j = 0; j < kJ; ++j) acc[i][j] = mfma16(vec_bf16x8(a[i]), vec_bf16x8(b[j]), acc[i][j]);
+          for (int w = 0; w < kWaves; ++w) sum += red[((w * 4 + (jr >> 4)) * 16 + (jr & 15)) * 17 + t];
+          const int sl = j / r;
+          store_z(p.zpad + int64_t(m0 + order[first + t]) * zw + sl * kZSlice + (j - sl * r), uint16_t(f32_to_bf16(sum)));
         }
       }
-      // A(kt + 1) and x(kt + 1) have landed once at most x(kt + 2) is outstanding.
-      wait_vm<kXCopies>();
-      lds_barrier();
+      __syncthreads();  // red is reused by the next pass
     }
-    wait_vm<0>();  // the requests past the end
-    // acc[i][j][e] = z[token m0 + wm*128 + 16i + 4g + e][pass column wn*48 + 16j + c]
-    if (busy) {
-#pragma unroll
-      for (int j = 0; j < kJ; ++j) {
-        const int e = colmap[wn * 48 + j * 16 + c];
-        if (e < 0) continue;
-        const int gd = list[e >> 16];
-        const int zc = ((e >> 8) & 0xff) * kZSlice + (e & 0xff);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = wm * 128 + i * 16 + 4 * g + r;
-            if (row < count && tslot[row] == gd)
-              p.zpad[int64_t(m0 + row) * zw + zc] = uint16_t(f32_to_bf16(acc[i][j][r]));
-          }
-      }
-    }
-    __syncthreads();  // colmap and the LDS slots are reused by the next pass
   }
-  // Publish: every thread's z stores are performed at device scope before the
-  // flag carries the call's tag.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // Publish: every thread's z stores have completed (sc1: at device scope)
+  // before the flag carries the call's tag (asm with a memory clobber, so the
+  // compiler keeps the flag store after it).
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
   __syncthreads();
-  if (tid == 0) __hip_atomic_store(p.zflags + mt, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(p.zflags + mt * p.zparts + q, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Waits until the z rows of M-tile mt carry the call's tag (their producer
@@ -439,10 +450,12 @@ __device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, uint32
 // at device scope would invalidate the whole L2 of the XCD under the other
 // workgroups' feet.
 __device__ __forceinline__ void wait_z(const PrefillParams& p, int mt, uint32_t tag) {
-  if (threadIdx.x == 0) {
-    // Bounded (about a quarter second): a workgroup never waits forever,
-    // whatever the launch order; giving up is reported in the status word.
-    for (int spins = 0; __hip_atomic_load(p.zflags + mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag; ++spins) {
+  if (threadIdx.x < p.zparts) {
+    // One thread per producer of the tile. Bounded (about a quarter second):
+    // a workgroup never waits forever, whatever the launch order; giving up
+    // is reported in the status word.
+    const uint32_t* flag = p.zflags + mt * p.zparts + threadIdx.x;
+    for (int spins = 0; __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag; ++spins) {
       if (spins > (1 << 20)) {
         __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
@@ -488,8 +501,8 @@ __device__ __forceinline__ void round_bias(const PrefillParams& p, f32x4 (&acc)[
     }
 }
 
-// Block ids below mtiles (LoRA launches only) produce the tiles' z rows;
-// the others are GEMM tiles, M-tile b % mtiles on consecutive ids.
+// Block ids below mtiles * zparts (LoRA launches only) produce the tiles' z
+// rows; the others are GEMM tiles, M-tile b % mtiles on consecutive ids.
 template <bool kLora>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) char xring[kXD * kXBytes];
@@ -497,10 +510,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(2048))) float table[512];  // [byte] -> (code[byte >> 4], code[byte & 15])
   __shared__ __attribute__((aligned(16))) int tslot[kLora ? kBM : 1];
   __shared__ int list[kLora ? kMaxList + 1 : 1];
-  __shared__ int cum[kLora ? kMaxList + 1 : 1];
-  __shared__ int colmap[kLora ? kBN : 1];
-  __shared__ int mrank[kLora ? kMaxList : 1];
-  __shared__ int mstride[kLora ? kMaxList : 1];
+  __shared__ int order[kLora ? kBM : 1];  // z producer: tile rows sorted by slot
+  __shared__ int mrank[kLora ? kMaxList + 1 : 1];
+  __shared__ int mstride[kLora ? kMaxList + 1 : 1];
   __shared__ float mscale[kLora ? kMaxList : 1];
   __shared__ int64_t mboff[kLora ? kMaxList : 1];
   const int tid = threadIdx.x;
@@ -508,12 +520,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   uint32_t tag = 0;
   if constexpr (kLora) {
     tag = __builtin_amdgcn_readfirstlane(epoch_tag(p.ce));
-    if (b < p.mtiles) {
-      produce_z(p, b, tag, xring, &wdec[0][0], tslot, list, colmap, cum);
+    if (b < p.mtiles * p.zparts) {
+      // (The slot metadata arrays double as the producer's sort counters; the
+      // idle x ring holds the partial tiles.)
+      produce_z(p, b / p.zparts, b % p.zparts, tag, tslot, list, order, mrank, mstride, reinterpret_cast<float*>(xring));
       depart(p, tag);
       return;
     }
-    b -= p.mtiles;
+    b -= p.mtiles * p.zparts;
   }
   const int mt = b % p.mtiles;
   const int nt = b / p.mtiles;
@@ -702,37 +716,53 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       }
     };
     // B fragments of slot d as the MFMA's A operand: feature wn0 + 16j + c,
-    // k-group g of ranks 0..31 (l0) and 32..63 (l1).
-    auto load_b = [&](int d, bf16x8 (&l0)[kJ], bf16x8 (&l1)[kJ]) {
+    // k-group g of ranks 0..31 (b0) and 32..63 (b1). Requested raw from
+    // clamped, readable places (a select on a load result would wait for it)
+    // and masked where used: past the row stride or the rank, and past N.
+    auto request_b = [&](int d, uint4 (&b0)[kJ], uint4 (&b1)[kJ]) {
       const int br = mstride[d];
       const uint16_t* bg = p.b_store + mboff[d];
       const bool two = mrank[d] > 32;
 #pragma unroll
       for (int j = 0; j < kJ; ++j) {
-        const int n = wn0 + j * 16 + c;
-        uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-        if (n < p.n) v0 = load_b8(bg + int64_t(n) * br, g * 8, br);
-        if (two && n < p.n) v1 = load_b8(bg + int64_t(n) * br, 32 + g * 8, br);
-        l0[j] = as_bf16x8(v0);
-        l1[j] = as_bf16x8(v1);
+        const uint16_t* row = bg + int64_t(min(wn0 + j * 16 + c, p.n - 1)) * br;
+        b0[j] = b_raw(row, br, g * 8);
+        if (two) b1[j] = b_raw(row, br, 32 + g * 8);
       }
     };
-    bf16x8 l0[kJ], l1[kJ];  // B fragments of the slot being applied (slot 0 first)
-    wait_z(p, mt, tag);
-    load_zs(0);
-    if (nd > 0) load_b(0, l0, l1);
-    round_bias(p, acc, wn0, g);
+    auto b_frag = [&](const uint4& raw, int d, int kk, int j) {
+      const int keep = (wn0 + j * 16 + c < p.n) ? min(mstride[d], mrank[d]) - kk : 0;
+      return as_bf16x8(keep_first(raw, keep));
+    };
     // Routes of this lane's eight tokens.
     int rslot[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) rslot[i] = tslot[wm * 128 + i * 16 + c];
+    // The next distinct slot after d taken by any of this wave's tokens (nd: none).
+    auto next_live = [&](int d) {
+      for (++d; d < nd; ++d) {
+        const int gd = list[d];
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) any |= rslot[i] == gd;
+        if (__ballot(any) != 0) break;
+      }
+      return d;
+    };
+    const int first = next_live(-1);
+    uint4 cb0[kJ], cb1[kJ], nb0[kJ], nb1[kJ];  // B of the slot being applied and of the next one
+    wait_z(p, mt, tag);
     uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle (the ring is idle)
     for (int s = 0; s < p.slices; ++s) {
       const int lo = p.slice_offsets[s];
       const int hi = p.slice_offsets[s + 1];
-      if (s > 0) {
-        __syncthreads();  // the previous slice's readers of zs are done
-        load_zs(s);
+      if (s > 0) __syncthreads();  // the previous slice's readers of zs are done
+      // The slice's z rows (the one place these untracked loads are made), and
+      // for slice 0 the first slot's B, requested before the base rounding.
+      load_zs(s);
+      if (s == 0) {
+        if (first < nd) request_b(first, cb0, cb1);
+        round_bias(p, acc, wn0, g);
       }
       wait_vm<0>();  // the z loads (and anything requested after them)
 #pragma unroll
@@ -747,16 +777,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       const bool inside = lo <= wn0 && wn0 + 48 <= hi;
       // delta[n][m] = sum_j B_g[n][j] z[m][j] for the wave's 128 tokens x 48
       // features, added with the reference's two roundings to the tokens
-      // routed to g and the features of slice s.
-      for (int d = 0; d < nd; ++d) {
+      // routed to g and the features of slice s. The next slot's B is
+      // requested before this slot's MFMAs, so its latency is hidden.
+      if (s > 0 && first < nd) request_b(first, cb0, cb1);
+      for (int d = first; d < nd;) {
+        const int dn = next_live(d);
+        if (dn < nd) request_b(dn, nb0, nb1);
         const int gd = list[d];
-        bool any = false;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) any |= rslot[i] == gd;
-        if (__ballot(any) == 0) continue;  // none of this wave's tokens takes slot d
-        if (d > 0 || s > 0) load_b(d, l0, l1);
         const bool two = mrank[d] > 32;
         const float scale = mscale[d];
+        bf16x8 l0[kJ], l1[kJ];
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+          l0[j] = b_frag(cb0[j], d, g * 8, j);
+          l1[j] = two ? b_frag(cb1[j], d, 32 + g * 8, j) : as_bf16x8(make_uint4(0, 0, 0, 0));
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const bool mine = rslot[i] == gd;
@@ -781,6 +816,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
               if (inside || (n >= lo && n < hi)) acc[i][j][e] += t[e];
             }
           }
+        }
+        d = dn;
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+          cb0[j] = nb0[j];
+          cb1[j] = nb1[j];
         }
       }
     }
@@ -850,11 +891,20 @@ namespace {
 int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 }  // namespace
 
-// Workspace: the control header (call epoch), one z flag per 256-token tile
-// at a fixed place (so a flag word only ever holds tags, whatever the shapes
-// of earlier calls on the workspace), the z rows (m x slices x 64 bf16), then
-// room for the fp32 block scales of a double-quant weight.
-constexpr int64_t kMaxTiles = kFlagRegion / 4;
+// Workspace: the control header (call epoch), the z flags (one per producer,
+// zparts per 256-token tile) at a fixed place (so a flag word only ever holds
+// tags, whatever the shapes of earlier calls on the workspace), the z rows
+// (m x slices x 64 bf16), then room for the fp32 block scales of a
+// double-quant weight.
+constexpr int64_t kMaxFlags = kFlagRegion / 4;
+constexpr int kMaxZParts = 64;
+
+// z producers per M-tile: about 128 in all (a unit of 16 tokens of one
+// adapter each, when routing spreads), at most 64 per tile, and within the
+// flag region.
+int zparts_for(int64_t mtiles) {
+  return int(std::max<int64_t>(1, std::min<int64_t>({kMaxZParts, 128 / mtiles, kMaxFlags / mtiles})));
+}
 
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int) {
   return kWorkspaceHeader + kFlagRegion + align256(m * slices * kZSlice * 2) + align256(n * (k / kNf4Block) * 4);
@@ -869,8 +919,8 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   LF_REQUIRE(!(lora || dq) || (workspace && workspace_bytes >= need && aligned16(workspace)),
              "workspace too small: need %lld bytes", (long long)need);
   LF_REQUIRE((m - 1) * x_stride * 2 + w->k * 2 < (int64_t(1) << 32), "x spans 4 GiB or more");
-  LF_REQUIRE((m + wide::kBM - 1) / wide::kBM <= kMaxTiles, "prefill handles at most %lld tokens per call",
-             (long long)(kMaxTiles * wide::kBM));
+  LF_REQUIRE((m + wide::kBM - 1) / wide::kBM <= kMaxFlags, "prefill handles at most %lld tokens per call",
+             (long long)(kMaxFlags * wide::kBM));
   auto s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   const float* scales = w->scales;
@@ -917,8 +967,9 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.status = reinterpret_cast<int*>(ws + kStatusOffset);
   }
   p.mtiles = int((m + wide::kBM - 1) / wide::kBM);
-  // LoRA launches put one z producer per M-tile ahead of the GEMM tiles.
-  const dim3 grid(unsigned(p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN) + (lora ? p.mtiles : 0)));
+  p.zparts = zparts_for(p.mtiles);
+  // LoRA launches put the z producers ahead of the GEMM tiles.
+  const dim3 grid(unsigned(p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN) + (lora ? p.mtiles * p.zparts : 0)));
   if (lora) hipLaunchKernelGGL((wide::gemm_kernel<true>), grid, dim3(wide::kThreads), 0, s, p);
   else hipLaunchKernelGGL((wide::gemm_kernel<false>), grid, dim3(wide::kThreads), 0, s, p);
   LF_HIP(hipGetLastError());
