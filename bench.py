@@ -23,7 +23,8 @@ benchmarks/check_qwen35_nf4_ops.py:11-41):
               with the exact-weights decode arithmetic;
   c2          BF16 row_shrink + row_expand, 64 tokens, 32 x rank 16;
   c3          NF4 + double-quant SwiGLU MLP 4096 / 12288 (gate/up, SwiGLU,
-              down), 16 rank-8 adapters, B = 1 / 8 / 64;
+              down), 16 rank-8 adapters, B = 1 / 8 / 64; c3_fused_* runs the
+              SwiGLU in the gate/up kernel's epilogue (two launches);
   c4          NF4 4096^2, 256 tokens, 128 retained-rank adapters
               (ranks {4..64}), Zipf(1.1) routing;
   c5          prefill M = 2048, K = 4096, N = 11008, NF4 + double quant,
@@ -409,7 +410,12 @@ def c3_items(device, reps: int, copies: int = 6):
                 silu_mul(gu_out, out=h)
                 nf4_lora_linear(h, q2, s2, lora=l2, out=y)
 
-            return fn
+            def fused():
+                # The SwiGLU in the gate/up epilogue (decode batches): two launches.
+                nf4_lora_linear(x, q1, s1, lora=l1, out=h, swiglu=True)
+                nf4_lora_linear(h, q2, s2, lora=l2, out=y)
+
+            return fn, fused
 
         # Algorithmic bytes: packed weights, uint8 absmax codes, fp32 second-level
         # scales and code2 of both weights, the adapters used, and the activations
@@ -420,9 +426,12 @@ def c3_items(device, reps: int, copies: int = 6):
         base = q_bytes + nblocks + absmax2 + 2 * 256 * 4
         act = batch * (hidden * 2 * 2 + inter * 2 * 2)
         work = base + 786432 * used + act
+        chains = [chain(m) for m in mlps]
         name = f"c3_b{batch}"
-        items.append(Timed(name, [chain(m) for m in mlps], reps, work))
+        items.append(Timed(name, [c[0] for c in chains], reps, work))
         meta[name] = dict(batch=batch, adapters_used=used, launches_per_call=3)
+        items.append(Timed(f"c3_fused_b{batch}", [c[1] for c in chains], reps, work))
+        meta[f"c3_fused_b{batch}"] = dict(batch=batch, adapters_used=used, launches_per_call=2, swiglu="gate/up epilogue")
 
     for batch in (1, 8, 64):
         per_batch(batch)

@@ -50,6 +50,22 @@ struct Tile {
   static_assert(kDma * (kDepth - 1) < 64, "vmcnt range");
 };
 
+// bf16(silu(g)) * u in fp32 (the caller's store rounds the product): silu
+// as g / (1 + e^-g), the form of the reference's activation.
+__device__ __forceinline__ float silu_times(float g, float u) {
+  const float act = g / (1.0f + expf(-g));
+  return round_bf16(act) * u;
+}
+
+// Global output row of local row j (0 .. R - 1) of a row group whose first
+// R / 2 rows start at lo and the others at hi (hi = lo + R / 2 for a plain
+// group; in SwiGLU-output mode lo is the group's first gate row and hi the
+// matching up row, hi = lo + n / 2).
+template <class TL>
+__device__ __forceinline__ int grow(int lo, int hi, int j) {
+  return j < TL::kR / 2 ? lo + j : hi + (j - TL::kR / 2);
+}
+
 struct GemvParams {
   const uint16_t* x;
   int64_t x_stride;
@@ -63,6 +79,7 @@ struct GemvParams {
   uint16_t* y;
   int64_t y_stride;
   int row_groups;  // n / R
+  int gated_half;  // SwiGLU output: n / 2 (a group's rows: R / 2 gate rows and the matching up rows), else 0
   // LoRA (kLora variants only).
   const uint16_t* a_store;
   const int64_t* a_offsets;
@@ -731,7 +748,7 @@ struct ExpandB {
 
 template <class TL>
 __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMeta* tm, ExpandB<TL>& b, int d0,
-                                               int row0, int lane) {
+                                               int lo, int hi, int lane) {
   const int n = lane & 15;
   const int kg = lane >> 4;
   const int nd = tm->nd;
@@ -745,7 +762,7 @@ __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMe
       // Raw 16 bytes only: the shift/mask (b8_fix) is applied where the
       // fragments are used, so nothing waits for these loads here.
       b.bf[q][r] = *reinterpret_cast<const uint4*>(
-          b8_at(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row0 + r * 16 + n, 8 * kg, live).src);
+          b8_at(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], grow<TL>(lo, hi, r * 16 + n), 8 * kg, live).src);
   }
 }
 
@@ -754,7 +771,7 @@ __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMe
 // waves do this before waiting for z, so the VALU work is off the path.
 template <class TL>
 __device__ __forceinline__ void expand_b_fix(const GemvParams& p, const TileMeta* tm, ExpandB<TL>& b, int d0,
-                                             int row0, int lane) {
+                                             int lo, int hi, int lane) {
   const int n = lane & 15;
   const int kg = lane >> 4;
   const int nd = tm->nd;
@@ -772,7 +789,7 @@ __device__ __forceinline__ void expand_b_fix(const GemvParams& p, const TileMeta
       const int boff = int(tm->dboff[d] & 7);
 #pragma unroll
       for (int r = 0; r < TL::kRT; ++r)
-        b.bf[q][r] = b8_fix(b.bf[q][r], B8{nullptr, (boff + (row0 + r * 16 + n) * st + 8 * kg) & 7, cnt});
+        b.bf[q][r] = b8_fix(b.bf[q][r], B8{nullptr, (boff + grow<TL>(lo, hi, r * 16 + n) * st + 8 * kg) & 7, cnt});
     }
   }
 }
@@ -780,16 +797,16 @@ __device__ __forceinline__ void expand_b_fix(const GemvParams& p, const TileMeta
 // Waits (LDS flag) for the LoRA wave's slot list, then requests this wave's
 // first batch of B fragments.
 template <class TL>
-__device__ __forceinline__ void expand_b_first(const GemvParams& p, const char* lds7, ExpandB<TL>& b, int row0,
-                                               int wave, int lane) {
+__device__ __forceinline__ void expand_b_first(const GemvParams& p, const char* lds7, ExpandB<TL>& b, int lo,
+                                               int hi, int wave, int lane) {
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds7 + LoraLds<TL>::kMeta);
   while (*(const volatile __attribute__((address_space(3))) int*)(&tm->ready) == 0) __builtin_amdgcn_s_sleep(1);
-  expand_b_batch<TL>(p, tm, b, wave, row0, lane);
+  expand_b_batch<TL>(p, tm, b, wave, lo, hi, lane);
 }
 
 template <class TL>
 __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& b, const int (&bounds)[4],
-                            f32x4 (&dacc)[TL::kRT][TL::kTT], int row0, int wave, int lane) {
+                            f32x4 (&dacc)[TL::kRT][TL::kTT], int lo, int hi, int wave, int lane) {
   using L = LoraLds<TL>;
   constexpr int RT = TL::kRT;
   constexpr int TT = TL::kTT;
@@ -803,17 +820,17 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
     for (int t = 0; t < TT; ++t) dacc[r][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
   const int nd = tm->nd;
   int cs[RT];  // slice of this lane's column in each row tile
+  auto slice_of = [&](int col) { return int(p.slices > 1 && col >= bounds[1]) + int(p.slices > 2 && col >= bounds[2]); };
 #pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    const int col = row0 + r * 16 + n;
-    cs[r] = int(p.slices > 1 && col >= bounds[1]) + int(p.slices > 2 && col >= bounds[2]);
-  }
-  const int s_lo = int(p.slices > 1 && row0 >= bounds[1]) + int(p.slices > 2 && row0 >= bounds[2]);
-  const int s_hi = int(p.slices > 1 && row0 + TL::kR - 1 >= bounds[1]) + int(p.slices > 2 && row0 + TL::kR - 1 >= bounds[2]);
+  for (int r = 0; r < RT; ++r) cs[r] = slice_of(grow<TL>(lo, hi, r * 16 + n));
+  // Slices the group's rows touch: its smallest row is lo, its largest hi + R / 2 - 1.
+  const int top = hi + TL::kR / 2 - 1;
+  const int s_lo = int(p.slices > 1 && lo >= bounds[1]) + int(p.slices > 2 && lo >= bounds[2]);
+  const int s_hi = int(p.slices > 1 && top >= bounds[1]) + int(p.slices > 2 && top >= bounds[2]);
   for (int d0 = wave; d0 < nd; d0 += kSlotBatch * kExpandWaves) {
     if (d0 != wave) {
-      expand_b_batch<TL>(p, tm, b, d0, row0, lane);
-      expand_b_fix<TL>(p, tm, b, d0, row0, lane);
+      expand_b_batch<TL>(p, tm, b, d0, lo, hi, lane);
+      expand_b_fix<TL>(p, tm, b, d0, lo, hi, lane);
     }
 #pragma unroll
     for (int q = 0; q < kSlotBatch; ++q) {
@@ -837,7 +854,7 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
           for (int r = 0; r < RT; ++r) {
             uint4 fixed = b.bf[q][r];  // ranks 0..31: shifted and masked already
             if (h == 1) {
-              const B8 b8 = b8_at(p, tm->dboff[d], tm->dstride[d], rk, row0 + r * 16 + n, 32 + 8 * kg, true);
+              const B8 b8 = b8_at(p, tm->dboff[d], tm->dstride[d], rk, grow<TL>(lo, hi, r * 16 + n), 32 + 8 * kg, true);
               fixed = b8_fix(*reinterpret_cast<const uint4*>(b8.src), b8);
             }
             const uint4 bb = cs[r] == s ? fixed : make_uint4(0, 0, 0, 0);
@@ -859,14 +876,14 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
 // wave's range read valid addresses of block kb (their scale is zeroed when
 // used). kb must be a valid block.
 template <class TL>
-__device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int row0, int t0, int mt, int kb,
+__device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int lo, int hi, int t0, int mt, int kb,
                                             int kend, int lane) {
   const int nblk = p.k >> 6;
   {
     const int b = lane / (2 * TL::kR);
     const int r = (lane >> 1) % TL::kR;
     const int blk = (lane < 2 * TL::kR * TL::kSB && kb + b < kend) ? kb + b : kb;
-    copy16(p.q + int64_t(row0 + r) * (p.k >> 1) + blk * 32 + (lane & 1) * 16, slot);
+    copy16(p.q + int64_t(grow<TL>(lo, hi, r)) * (p.k >> 1) + blk * 32 + (lane & 1) * 16, slot);
   }
 #pragma unroll
   for (int d = 0; d < TL::kXDma; ++d) {
@@ -883,7 +900,7 @@ __device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int
     const int b = lane / TL::kR;
     const int r = lane % TL::kR;
     const int blk = (lane < TL::kR * TL::kSB && kb + b < kend) ? kb + b : kb;
-    copy4(p.scales + int64_t(row0 + r) * nblk + (blk < nblk ? blk : 0), slot + TL::kWBytes + TL::kXBytes);
+    copy4(p.scales + int64_t(grow<TL>(lo, hi, r)) * nblk + (blk < nblk ? blk : 0), slot + TL::kWBytes + TL::kXBytes);
   }
 }
 
@@ -900,10 +917,14 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t pt[kExact ? 4 : 256 * kCopies];
   __shared__ float red[kLora ? kProd * 192 : 1];
   __shared__ int prod_done;  // contraction waves that have written their first-unit partials
+  __shared__ f32x4 up_vals[RT == 2 ? TL::kTT * 64 : 1];  // SwiGLU output: the up tile's final values
 
   const int rg = blockIdx.x % p.row_groups;
   const int tile = blockIdx.x / p.row_groups;
-  const int row0 = rg * TL::kR;
+  // The group's rows: R contiguous rows, or in SwiGLU-output mode R / 2 gate
+  // rows and the R / 2 up rows of the same features.
+  const int lo = p.gated_half ? rg * (TL::kR / 2) : rg * TL::kR;
+  const int hi = p.gated_half ? p.gated_half + lo : lo + TL::kR / 2;
   const int t0 = tile * 32;
   const int mt = min(32, p.m - t0);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -955,7 +976,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       else __builtin_amdgcn_s_sleep(16);
     }
 #pragma unroll
-    for (int s = 0; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, row0, t0, mt, stage_kb(s), kend, lane);
+    for (int s = 0; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, lo, hi, t0, mt, stage_kb(s), kend, lane);
   } else if constexpr (kLora) {
     // The LoRA wave: the epoch and the first loads of its metadata chains
     // (vector loads: the barriers below wait only for scalar loads and LDS,
@@ -1038,7 +1059,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       read_frags<TL>(nxt, ring_base + ((s + 1) % D) * TL::kStage, n, g);
     }
     if (s + D < nst)
-      issue_stage<TL>(p, myring + (s % D) * TL::kStage, row0, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
+      issue_stage<TL>(p, myring + (s % D) * TL::kStage, lo, hi, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
     contract<TL, kExact>(cur, kb0 + s * TL::kSB, kend, acc, table, ptl);
     if (more) {
       settle(nxt);
@@ -1065,11 +1086,11 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       lora_gather<TL>(p, lora7, t0, mt, __builtin_amdgcn_readfirstlane(epoch) + 1u, lane);
       departed = depart_issue(p.ce, lane);  // after the last partial load: nothing waits for it until the end
     } else {
-      expand_b_first<TL>(p, lora7, eb, row0, wave, lane);
-      expand_b_fix<TL>(p, reinterpret_cast<const TileMeta*>(lora7 + LoraLds<TL>::kMeta), eb, wave, row0, lane);
+      expand_b_first<TL>(p, lora7, eb, lo, hi, wave, lane);
+      expand_b_fix<TL>(p, reinterpret_cast<const TileMeta*>(lora7 + LoraLds<TL>::kMeta), eb, wave, lo, hi, lane);
     }
     lds_barrier();  // z and the tile metadata are in LDS
-    if (wave < kBase) expand_mfma<TL>(p, lora7, eb, bounds, dacc, row0, wave, lane);
+    if (wave < kBase) expand_mfma<TL>(p, lora7, eb, bounds, dacc, lo, hi, wave, lane);
     if (wave < kBase) {
       wait_vm<0>();  // stages past the wave's blocks (short K) may still be landing in the ring
       f32x4* base_tiles = reinterpret_cast<f32x4*>(myring);
@@ -1091,9 +1112,11 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       for (int t = 0; t < TT; ++t) base_tiles[(r * TT + t) * 64 + lane] = acc[r][t];
   }
   lds_barrier();
-  if (wave < kTiles) {
-    const int r = wave / TT;
-    const int t = wave % TT;
+  const bool summer = wave < kTiles;  // wave c sums tile (r, t) = (c / TT, c % TT)
+  const int r = summer ? wave / TT : 0;
+  const int t = summer ? wave % TT : 0;
+  f32x4 out = {0.f, 0.f, 0.f, 0.f};  // the tile's final values (bf16, as stored)
+  if (summer) {
     f32x4 sum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kBase; ++w) {
@@ -1111,18 +1134,43 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       }
     }
     const TileMeta* tm = reinterpret_cast<const TileMeta*>(lora7 + LoraLds<TL>::kMeta);
-    const int col = row0 + r * 16 + n;
+    const int col = grow<TL>(lo, hi, r * 16 + n);
     const float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = t * 16 + 4 * g + e;  // tile token
-      if (i < mt) {
-        float v = round_bf16(sum[e]);
-        if (p.bias) v = round_bf16(v + bias);
-        if constexpr (kLora) {
-          if (tm->g[i] >= 0) v += round_bf16(dsum[e] * tm->scale[i]);  // the store rounds
-        }
-        p.y[int64_t(t0 + i) * p.y_stride + col] = uint16_t(f32_to_bf16(v));
+      float v = round_bf16(sum[e]);
+      if (p.bias) v = round_bf16(v + bias);
+      if constexpr (kLora) {
+        if (i < mt && tm->g[i] >= 0) v += round_bf16(dsum[e] * tm->scale[i]);
+      }
+      out[e] = round_bf16(v);
+      if (!p.gated_half && i < mt) p.y[int64_t(t0 + i) * p.y_stride + col] = uint16_t(f32_to_bf16(v));
+    }
+  }
+  if (p.gated_half) {
+    // SwiGLU output h[token][f] = bf16(bf16(silu(gate)) * up) for the group's
+    // features f = lo .. lo + R / 2 (the reference's activation after both
+    // LoRA adds, benchmarks/qwen35_decode_silu.py:60-61).
+    f32x4 up = {0.f, 0.f, 0.f, 0.f};
+    bool gate = false;
+    if constexpr (RT == 1) {
+      // Lanes n < 8 hold gate rows lo + n, lanes n + 8 the matching up rows.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) up[e] = __shfl_xor(out[e], 8, 64);
+      gate = summer && n < 8;
+    } else {
+      // Tile r = 0 holds the gate rows lo .. lo + 15, tile r = 1 the up rows.
+      if (summer && r == 1) up_vals[t * 64 + lane] = out;
+      lds_barrier();
+      if (summer && r == 0) up = up_vals[t * 64 + lane];
+      gate = summer && r == 0;
+    }
+    if (gate) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = t * 16 + 4 * g + e;
+        if (i < mt) p.y[int64_t(t0 + i) * p.y_stride + lo + n] = uint16_t(f32_to_bf16(silu_times(out[e], up[e])));
       }
     }
   }
@@ -1202,7 +1250,7 @@ int64_t gemv_workspace_bytes(int64_t, int64_t, int64_t, int, int) { return kWork
 // Fused NF4 + multi-LoRA linear for 1..64 tokens with fp32 block scales.
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
-                    bool exact, void* stream) {
+                    bool exact, bool swiglu, void* stream) {
   LF_REQUIRE(m >= 1 && m <= 64, "decode path handles 1..64 tokens");
   LF_REQUIRE(w->scales != nullptr, "decode takes fp32 block scales (prepare double-quant scales first)");
   const GemvPlan pl = gemv_plan(m, w->n, w->k, device_cus(), lora ? lora->num_slices * lora->max_rank : 1);
@@ -1220,6 +1268,7 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   p.y = y;
   p.y_stride = y_stride;
   p.row_groups = pl.row_groups;
+  p.gated_half = swiglu ? int(w->n / 2) : 0;  // n % 32 == 0: R / 2 divides n / 2
   if (lora) {
     LF_REQUIRE(workspace && workspace_bytes >= kWorkspaceHeader, "workspace too small: need %lld bytes",
                (long long)kWorkspaceHeader);

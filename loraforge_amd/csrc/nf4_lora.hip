@@ -7,7 +7,7 @@ namespace lf {
 int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
-                    bool exact, void* stream);
+                    bool exact, bool swiglu, void* stream);
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
@@ -26,7 +26,8 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
                                   const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                                   void* workspace, int64_t workspace_bytes, int32_t flags, void* stream) {
   LF_REQUIRE(w != nullptr, "weight descriptor required");
-  LF_REQUIRE((flags & ~LF_EXACT_WEIGHTS) == 0, "unknown flags");
+  LF_REQUIRE((flags & ~(LF_EXACT_WEIGHTS | LF_SWIGLU_OUTPUT)) == 0, "unknown flags");
+  const bool swiglu = (flags & LF_SWIGLU_OUTPUT) != 0;
   LF_REQUIRE(m >= 0 && m < (int64_t(1) << 31), "token count out of range");
   const int64_t n = w->n, k = w->k;
   LF_REQUIRE(n > 0 && k > 0 && n % 64 == 0 && k % 64 == 0, "weight shape must contain two positive multiples of 64");
@@ -37,7 +38,10 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
              "scales or a complete double-quant state required");
   LF_REQUIRE(lf::aligned16(x) && x_stride >= k && x_stride % 8 == 0, "x must be 16-byte aligned with row stride %% 8 == 0");
   LF_REQUIRE(lf::aligned16(w->qweight), "packed weight must be 16-byte aligned");
-  LF_REQUIRE(y_stride >= n, "output row stride must cover the output width");
+  LF_REQUIRE(y_stride >= (swiglu ? n / 2 : n), "output row stride must cover the output width");
+  LF_REQUIRE(!swiglu || (m <= lf::kDecodeMaxTokens && n % 32 == 0),
+             "SwiGLU output needs a decode batch (M <= 64) and N a multiple of 32");
+  LF_REQUIRE(!swiglu || !lora || lora->num_slices == 2, "SwiGLU output with LoRA needs the two gate/up slices");
   if (lora) {
     LF_REQUIRE(lora->num_slices >= 1 && lora->num_slices <= 3, "num_slices must be in 1..3");
     LF_REQUIRE(lora->max_rank >= 1 && lora->max_rank <= 64, "max_rank must be in 1..64");
@@ -53,7 +57,7 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
     LF_REQUIRE(w->scales != nullptr,
                "decode (M <= 64) takes fp32 block scales: build them with lf_nf4_prepare_scales_dq");
     return lf::launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
-                               (flags & LF_EXACT_WEIGHTS) != 0, stream);
+                               (flags & LF_EXACT_WEIGHTS) != 0, swiglu, stream);
   }
   return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, stream);
 }

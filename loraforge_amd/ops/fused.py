@@ -260,7 +260,17 @@ def _lora_struct(lora: LoraBatch, m: int, k: int, n: int, device):
 
 @ExperimentalAPI(reason="gfx950 fused NF4 + multi-LoRA linear; caller-owned device metadata.")
 def nf4_lora_linear(
-    x, qweight, state, *, scales=None, bias=None, lora: LoraBatch | None = None, out=None, workspace=None, exact=False
+    x,
+    qweight,
+    state,
+    *,
+    scales=None,
+    bias=None,
+    lora: LoraBatch | None = None,
+    out=None,
+    workspace=None,
+    exact=False,
+    swiglu=False,
 ):
     """``y = bf16(x @ dequant(W)^T) (+bias)``, then the per-token LoRA delta.
 
@@ -277,6 +287,13 @@ def nf4_lora_linear(
     kernel (<= 64 tokens) contracts ``bf16(code[nibble])`` on MFMA and applies
     each fp32 block scale to the block's partial sum; ``exact=True`` makes it
     multiply the exact weights too (bit-identical W, slower).
+
+    ``swiglu=True``: the weight is a merged gate/up projection (gate rows
+    ``0 .. N/2``, up rows ``N/2 .. N``; with LoRA, slices ``[0, N/2, N]``) and
+    the result is ``h = bf16(bf16(silu(gate)) * up)``, ``[..., N/2]``, of the
+    LoRA-updated bf16 gate and up outputs. Batches of up to 32 tokens compute
+    it in the decode kernel's epilogue (no gate/up round trip, no second
+    launch); larger ones run the linear and then ``silu_mul``.
     """
     import torch
 
@@ -303,11 +320,30 @@ def nf4_lora_linear(
         raise ValueError("x rows must be 16-byte aligned with a stride multiple of 8; qweight 16-byte aligned")
     if bias is not None:
         vector(bias, "bias", torch.bfloat16, device, n)
+    width = n
+    if swiglu:
+        if n % 32:
+            raise ValueError("SwiGLU output needs N a multiple of 32")
+        if lora is not None and lora.num_slices != 2:
+            raise ValueError("SwiGLU output with LoRA needs the two gate/up slices")
+        width = n // 2
+        # Batches above 32 tokens run the linear and then the activation: their
+        # decode groups (32 rows, two token tiles) would take both gate/up
+        # slices' expand per workgroup, measured slower than the second launch
+        # (c3 at B = 64: 136 us fused against 134 us).
+        if m > 32:
+            from .activation import silu_mul
+
+            if out is not None and (out.dtype != torch.bfloat16 or out.shape != (*lead, width) or out.stride(-1) != 1):
+                raise ValueError("out must be bf16 [..., N/2] on the input device")
+            gate_up = nf4_lora_linear(x2, qweight, state, scales=scales, bias=bias, lora=lora, workspace=workspace, exact=exact)
+            h = silu_mul(gate_up, out=None if out is None else out.reshape(-1, width))
+            return h.reshape(*lead, width) if out is None else out
     if out is None:
-        out = torch.empty((*lead, n), dtype=torch.bfloat16, device=device)
-    elif out.dtype != torch.bfloat16 or out.shape != (*lead, n) or out.device != device or out.stride(-1) != 1:
-        raise ValueError("out must be bf16 [..., N] on the input device")
-    y2 = out.reshape(-1, n)
+        out = torch.empty((*lead, width), dtype=torch.bfloat16, device=device)
+    elif out.dtype != torch.bfloat16 or out.shape != (*lead, width) or out.device != device or out.stride(-1) != 1:
+        raise ValueError(f"out must be bf16 [..., {'N/2' if swiglu else 'N'}] on the input device")
+    y2 = out.reshape(-1, width)
     if y2.data_ptr() != out.data_ptr():
         raise ValueError("out must be viewable as [M, N]")
     distinct_output(out, (x, qweight, bias))
@@ -340,7 +376,7 @@ def nf4_lora_linear(
                 y2.stride(0),
                 workspace.data_ptr(),
                 workspace.numel(),
-                _lib.LF_EXACT_WEIGHTS if exact else 0,
+                (_lib.LF_EXACT_WEIGHTS if exact else 0) | (_lib.LF_SWIGLU_OUTPUT if swiglu else 0),
                 stream,
             )
         )
