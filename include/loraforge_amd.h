@@ -85,9 +85,12 @@ int lf_row_shrink(const uint16_t* x, const uint16_t* a, uint16_t* z, const int32
 int64_t lf_row_shrink_workspace_size(int64_t tokens, int64_t width, int64_t num_adapters,
                                      int32_t num_slices, int32_t max_rank);
 
-/* Test hook for lf_row_shrink only: K chunks past the first publish no
- * partials, so every summing workgroup gives up its (shortened) wait and
- * recomputes them; the output must not change. */
+/* Test hook (lf_row_shrink and lf_nf4_lora_linear): the producers publish
+ * nothing (row shrink: K chunks past the first store no partials; fused
+ * linear: decode shrink producers store no tagged partials, prefill z
+ * producers store no z and set no flag), so every consumer gives up its
+ * (shortened) bounded wait, recomputes what it waited for from x and A and
+ * sets the status word; the output must not change beyond rounding. */
 #define LF_TEST_WITHHOLD_PARTIALS 0x100
 
 /* lf_row_expand replaces the pybind `expand` of ops/csrc/lora_rows.cu:188-209

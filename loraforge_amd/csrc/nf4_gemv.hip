@@ -97,7 +97,9 @@ struct GemvParams {
   int kz;         // k-slices per token
   int kz_len;     // k per slice (multiple of 64)
   int producers;  // workgroups b < producers make units b, b + producers, ...
-  int* status;    // set to 1 when a bounded wait times out
+  int* status;    // set to 1 when a bounded wait for partials gave up (they were then recomputed)
+  int spin_limit; // polls of a bounded wait for partials
+  int withhold;   // test hook: producers publish nothing, so every wait gives up and recomputes
   CallEpoch ce;      // call tag: epoch + 1, moved on by the last workgroup
   uint64_t* zp;      // [units][zw] shrink partial sums as (tag << 32) | fp32 bits
 };
@@ -473,7 +475,7 @@ __device__ void publish_first_unit(const GemvParams& p, const float* red, const 
     if (jj < rows) {
       float v = 0.f;
       for (int w = 0; w < kProd; ++w) v += red[w * 192 + jj];
-      tagged_store(p.zp + partial_index(p, un, jj), v, tag);
+      if (!p.withhold) tagged_store(p.zp + partial_index(p, un, jj), v, tag);
     }
   }
 }
@@ -495,7 +497,7 @@ __device__ void produce_other_units(const GemvParams& p, uint32_t tag, int lane)
         unit_frags<false, kBatch>(p, un, j0, st0, 1, lane, f);
         c = unit_mfma(f, un, st0, 1, c);
       }
-      if (kg == 0 && j0 + jn < un.rows) tagged_store(p.zp + partial_index(p, un, j0 + jn), c[0], tag);
+      if (kg == 0 && j0 + jn < un.rows && !p.withhold) tagged_store(p.zp + partial_index(p, un, j0 + jn), c[0], tag);
     }
   }
 }
@@ -662,8 +664,28 @@ __device__ __forceinline__ int small_div(int a, uint32_t inverse) { return int((
 // registers, z[i][j] = bf16(sum), and stored slice padded into LDS (zero past
 // the rank). Entries of base-only tokens and past the rank are never waited
 // for or used. KZ (k-slices per token) is a power of two up to 16.
+// z value j of token t (slot g) before rounding: sum over K of
+// x[t][k] * A_g[j][k] (A rows packed at s * r, so value j is row j), in fp32.
+__device__ __forceinline__ float full_dot(const GemvParams& p, int t, int g, int j) {
+  const uint16_t* xr = p.x + int64_t(t) * p.x_stride;
+  const uint16_t* ar = p.a_store + p.a_offsets[g] + int64_t(j) * p.k;
+  float acc = 0.f;
+  for (int k = 0; k < p.k; k += 8) {
+    const uint4 xv = *reinterpret_cast<const uint4*>(xr + k);
+    const uint4 av = *reinterpret_cast<const uint4*>(ar + k);
+    const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t as[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = __builtin_fmaf(bf16_lo(xs[e]), bf16_lo(as[e]), acc);
+      acc = __builtin_fmaf(bf16_hi(xs[e]), bf16_hi(as[e]), acc);
+    }
+  }
+  return acc;
+}
+
 template <class TL, int KZ>
-__device__ void lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, uint32_t tag, int lane) {
+__device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, uint32_t tag, int lane) {
   using L = LoraLds<TL>;
   constexpr int kOut = 16 / KZ;  // values per lane and batch
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + L::kMeta);
@@ -685,6 +707,7 @@ __device__ void lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
       need[q] = q * 64 + lane < nout && tm->g[i] >= 0 && jv[q] < p.slices * tm->r[i];
     }
     uint64_t v[kOut][KZ];
+    bool gave_up = false;
     for (int spins = 0;; ++spins) {
 #pragma unroll
       for (int q = 0; q < kOut; ++q)
@@ -697,8 +720,8 @@ __device__ void lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
 #pragma unroll
         for (int ks = 0; ks < KZ; ++ks) ok = ok && (!need[q] || uint32_t(v[q][ks] >> 32) == tag);
       if (__all(ok)) break;
-      if (spins > kSpinLimit) {
-        if (lane == 0) __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (spins > p.spin_limit) {
+        gave_up = true;  // (cannot happen while producers run: they wait for nothing)
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -714,18 +737,42 @@ __device__ void lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
       const int s = int(j >= ri) + int(j >= 2 * ri) + int(j >= 3 * ri);  // slice of value j (3: past them)
       if (need[q] && s < p.slices) zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(z));
     }
+    if (gave_up) return true;
+  }
+  return false;
+}
+
+// After a wait gave up: every z value of the tile is recomputed from x and A
+// over the whole K (one compact loop, off the normal path; fp32 sums in
+// another order than the partials', so z may differ by a bf16 rounding); the
+// status word reports it.
+template <class TL>
+__device__ void lora_recompute(const GemvParams& p, char* lds, int t0, int mt, int lane) {
+  using L = LoraLds<TL>;
+  const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + L::kMeta);
+  uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
+  if (lane == 0) __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int o = lane; o < mt * p.zw; o += 64) {
+    const int i = o / p.zw;
+    const int j = o - i * p.zw;
+    const int ri = tm->r[i];
+    if (tm->g[i] < 0 || j >= p.slices * ri) continue;
+    const int s = j / ri;
+    zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(full_dot(p, t0 + i, tm->g[i], j)));
   }
 }
 
 template <class TL>
 __device__ void lora_gather(const GemvParams& p, char* lds, int t0, int mt, uint32_t tag, int lane) {
+  bool gave_up;
   switch (p.kz) {
-    case 1: lora_gather_kz<TL, 1>(p, lds, t0, mt, tag, lane); break;
-    case 2: lora_gather_kz<TL, 2>(p, lds, t0, mt, tag, lane); break;
-    case 4: lora_gather_kz<TL, 4>(p, lds, t0, mt, tag, lane); break;
-    case 8: lora_gather_kz<TL, 8>(p, lds, t0, mt, tag, lane); break;
-    default: lora_gather_kz<TL, 16>(p, lds, t0, mt, tag, lane); break;
+    case 1: gave_up = lora_gather_kz<TL, 1>(p, lds, t0, mt, tag, lane); break;
+    case 2: gave_up = lora_gather_kz<TL, 2>(p, lds, t0, mt, tag, lane); break;
+    case 4: gave_up = lora_gather_kz<TL, 4>(p, lds, t0, mt, tag, lane); break;
+    case 8: gave_up = lora_gather_kz<TL, 8>(p, lds, t0, mt, tag, lane); break;
+    default: gave_up = lora_gather_kz<TL, 16>(p, lds, t0, mt, tag, lane); break;
   }
+  if (gave_up) lora_recompute<TL>(p, lds, t0, mt, lane);
 }
 
 // Expand on MFMA, by the contraction waves (the LoRA wave finishes z last):
@@ -1250,7 +1297,7 @@ int64_t gemv_workspace_bytes(int64_t, int64_t, int64_t, int, int) { return kWork
 // Fused NF4 + multi-LoRA linear for 1..64 tokens with fp32 block scales.
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
-                    bool exact, bool swiglu, void* stream) {
+                    bool exact, bool swiglu, bool withhold, void* stream) {
   LF_REQUIRE(m >= 1 && m <= 64, "decode path handles 1..64 tokens");
   LF_REQUIRE(w->scales != nullptr, "decode takes fp32 block scales (prepare double-quant scales first)");
   const GemvPlan pl = gemv_plan(m, w->n, w->k, device_cus(), lora ? lora->num_slices * lora->max_rank : 1);
@@ -1294,6 +1341,8 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
     char* ws = static_cast<char*>(workspace);
     p.ce = call_epoch_of(ws);
     p.status = reinterpret_cast<int*>(ws + kStatusOffset);
+    p.withhold = withhold ? 1 : 0;
+    p.spin_limit = withhold ? 64 : kSpinLimit;
     p.zp = reinterpret_cast<uint64_t*>(ws + kPartialsOffset);
   }
   const dim3 grid(unsigned(pl.grid));

@@ -7,11 +7,11 @@ namespace lf {
 int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
-                    bool exact, bool swiglu, void* stream);
+                    bool exact, bool swiglu, bool withhold, void* stream);
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                            void* workspace, int64_t workspace_bytes, void* stream);
+                            void* workspace, int64_t workspace_bytes, bool withhold, void* stream);
 constexpr int64_t kDecodeMaxTokens = 64;
 }  // namespace lf
 
@@ -26,7 +26,8 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
                                   const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                                   void* workspace, int64_t workspace_bytes, int32_t flags, void* stream) {
   LF_REQUIRE(w != nullptr, "weight descriptor required");
-  LF_REQUIRE((flags & ~(LF_EXACT_WEIGHTS | LF_SWIGLU_OUTPUT)) == 0, "unknown flags");
+  LF_REQUIRE((flags & ~(LF_EXACT_WEIGHTS | LF_SWIGLU_OUTPUT | LF_TEST_WITHHOLD_PARTIALS)) == 0, "unknown flags");
+  const bool withhold = (flags & LF_TEST_WITHHOLD_PARTIALS) != 0;
   const bool swiglu = (flags & LF_SWIGLU_OUTPUT) != 0;
   LF_REQUIRE(m >= 0 && m < (int64_t(1) << 31), "token count out of range");
   const int64_t n = w->n, k = w->k;
@@ -57,9 +58,10 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
     LF_REQUIRE(w->scales != nullptr,
                "decode (M <= 64) takes fp32 block scales: build them with lf_nf4_prepare_scales_dq");
     return lf::launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
-                               (flags & LF_EXACT_WEIGHTS) != 0, swiglu, stream);
+                               (flags & LF_EXACT_WEIGHTS) != 0, swiglu, withhold, stream);
   }
-  return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, stream);
+  return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, withhold,
+                                     stream);
 }
 
 extern "C" int lf_nf4_lora_status(const void* workspace, void* stream, int32_t* status) {

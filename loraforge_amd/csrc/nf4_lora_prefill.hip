@@ -65,6 +65,8 @@ struct PrefillParams {
   int* status;  // set to 1 if a wait for z gives up (cannot happen while producers run first)
   int mtiles;
   int zparts;   // z producers per M-tile
+  int spin_limit;  // polls of the bounded wait for a producer's flag
+  int withhold;    // test hook: producers store nothing and set no flag, so consumers recompute z
 };
 
 __device__ __forceinline__ int swz(int row, int unit) { return row * 8 + (unit ^ (row & 7)); }
@@ -320,8 +322,8 @@ constexpr int kUnit = 16;        // tokens per unit
 constexpr int kUnitRows = 64;    // A rows per pass
 constexpr int kUnitSteps = 4;    // k steps of loads in flight per wave
 
-__device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, int q, uint32_t tag, int* tslot, int* list,
-                                          int* order, int* cnt, int* ustart, float* red) {
+__device__ void produce_units(const PrefillParams& p, int mt, int q, int* tslot, int* list, int* order, int* cnt,
+                              int* ustart, float* red) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -435,35 +437,60 @@ __device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, int q,
       __syncthreads();  // red is reused by the next pass
     }
   }
-  // Publish: every thread's z stores have completed (sc1: at device scope)
-  // before the flag carries the call's tag (asm with a memory clobber, so the
-  // compiler keeps the flag store after it).
+  // Every thread's z stores have completed (sc1: at device scope) when this
+  // returns (asm with a memory clobber, so the compiler keeps later stores
+  // after it).
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
   __syncthreads();
-  if (tid == 0) __hip_atomic_store(p.zflags + mt * p.zparts + q, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waits until the z rows of M-tile mt carry the call's tag (their producer
-// has a lower block id, so it has been dispatched before this workgroup).
-// The flag and the z rows are read with device-scope loads (coherent past
+// Producer (mt, q): its units, then its flag carries the call's tag.
+__device__ __forceinline__ void produce_z(const PrefillParams& p, int mt, int q, uint32_t tag, int* tslot, int* list,
+                                          int* order, int* cnt, int* ustart, float* red) {
+  if (p.withhold) return;  // test hook: the tile's consumers must recompute
+  produce_units(p, mt, q, tslot, list, order, cnt, ustart, red);
+  if (threadIdx.x == 0) __hip_atomic_store(p.zflags + mt * p.zparts + q, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until the z rows of M-tile mt carry the call's tag (their producers
+// have lower block ids, so they were dispatched before this workgroup).
+// The flags and the z rows are read with device-scope loads (coherent past
 // the caches of this CU and XCD), so no acquire fence is needed: an acquire
 // at device scope would invalidate the whole L2 of the XCD under the other
-// workgroups' feet.
-__device__ __forceinline__ void wait_z(const PrefillParams& p, int mt, uint32_t tag) {
+// workgroups' feet. Each wait is bounded (about a quarter second); a
+// producer that has not set its flag by then has its units recomputed here
+// (same arithmetic, so the same z bits), the status word records it, and the
+// tile's slot metadata, whose LDS the recomputation borrowed, is reloaded.
+// Returns whether it recomputed anything.
+__device__ bool wait_z(const PrefillParams& p, int mt, uint32_t tag, int* tslot, int* list, int* order, int* mrank,
+                       int* mstride, float* mscale, int64_t* mboff, float* red, uint32_t* missing) {
+  if (threadIdx.x < 2) missing[threadIdx.x] = 0;
+  __syncthreads();
   if (threadIdx.x < p.zparts) {
-    // One thread per producer of the tile. Bounded (about a quarter second):
-    // a workgroup never waits forever, whatever the launch order; giving up
-    // is reported in the status word.
     const uint32_t* flag = p.zflags + mt * p.zparts + threadIdx.x;
     for (int spins = 0; __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag; ++spins) {
-      if (spins > (1 << 20)) {
-        __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (spins > p.spin_limit) {
+        atomicOr(&missing[threadIdx.x >> 5], 1u << (threadIdx.x & 31));
         break;
       }
       __builtin_amdgcn_s_sleep(8);
     }
   }
   __syncthreads();
+  const uint64_t lost = uint64_t(missing[0]) | (uint64_t(missing[1]) << 32);
+  if (lost == 0) return false;
+  if (threadIdx.x == 0) __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int q = 0; q < p.zparts; ++q)
+    if ((lost >> q) & 1) produce_units(p, mt, q, tslot, list, order, mrank, mstride, red);
+  for (int d = threadIdx.x; d < list[kMaxList]; d += blockDim.x) {
+    const int gg = list[d];
+    mrank[d] = p.ranks[gg];
+    mstride[d] = p.b_strides[gg];
+    mscale[d] = p.lscales[gg];
+    mboff[d] = p.b_offsets[gg];
+  }
+  __syncthreads();
+  return true;
 }
 
 // 16 bytes of z rows in one device-scope (sc1) load, coherent past this
@@ -511,6 +538,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) int tslot[kLora ? kBM : 1];
   __shared__ int list[kLora ? kMaxList + 1 : 1];
   __shared__ int order[kLora ? kBM : 1];  // z producer: tile rows sorted by slot
+  __shared__ uint32_t zmissing[2];        // producers of the tile whose flag never came
   __shared__ int mrank[kLora ? kMaxList + 1 : 1];
   __shared__ int mstride[kLora ? kMaxList + 1 : 1];
   __shared__ float mscale[kLora ? kMaxList : 1];
@@ -751,7 +779,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
     };
     const int first = next_live(-1);
     uint4 cb0[kJ], cb1[kJ], nb0[kJ], nb1[kJ];  // B of the slot being applied and of the next one
-    wait_z(p, mt, tag);
+    wait_z(p, mt, tag, tslot, list, order, mrank, mstride, mscale, mboff, reinterpret_cast<float*>(xring), zmissing);
     uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle (the ring is idle)
     for (int s = 0; s < p.slices; ++s) {
       const int lo = p.slice_offsets[s];
@@ -912,7 +940,7 @@ int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int
 
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                            void* workspace, int64_t workspace_bytes, void* stream) {
+                            void* workspace, int64_t workspace_bytes, bool withhold, void* stream) {
   const int slices = lora ? lora->num_slices : 1;
   const bool dq = w->scales == nullptr;
   const int64_t need = prefill_workspace_bytes(m, w->n, w->k, slices, lora ? lora->max_rank : 1);
@@ -966,6 +994,8 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.ce = call_epoch_of(ws);
     p.status = reinterpret_cast<int*>(ws + kStatusOffset);
   }
+  p.withhold = withhold ? 1 : 0;
+  p.spin_limit = withhold ? 64 : (1 << 20);
   p.mtiles = int((m + wide::kBM - 1) / wide::kBM);
   p.zparts = zparts_for(p.mtiles);
   // LoRA launches put the z producers ahead of the GEMM tiles.
