@@ -300,8 +300,8 @@ def segments_of(routes, max_rows: int = 16):
     return np.array(indptr, np.int32), np.array(seg_slots, np.int32), np.array(order, np.int32)
 
 
-def decode_items(work: DecodeWorkload, reps: int):
-    """c1, the north-star sweep (with LoRA, base only, exact weights) and c2."""
+def decode_items(work: DecodeWorkload, reps: int, wanted=("c1", "north_star", "c2")):
+    """c1, the north-star sweep (with LoRA, base only, exact weights) and c2 (those in ``wanted``)."""
     import torch
 
     from loraforge_amd.ops import row_expand, row_shrink
@@ -309,6 +309,8 @@ def decode_items(work: DecodeWorkload, reps: int):
     items, meta = [], {}
 
     def add(name, batch, seed, *, lora=True, exact=False, null_frac=0.1, adapters=ADAPTERS):
+        if (name if name == "c1" else "north_star") not in wanted:
+            return
         x, slots, used = work.batch(batch, seed, null_frac=null_frac, adapters=adapters)
         used = used if lora else 0
         out = torch.empty(batch, work.n, dtype=torch.bfloat16, device=work.device)
@@ -322,6 +324,8 @@ def decode_items(work: DecodeWorkload, reps: int):
         add(f"base_only_b{b}", b, 731 + b, lora=False)
         add(f"exact_b{b}", b, 731 + b, exact=True)
 
+    if "c2" not in wanted:
+        return items, meta
     # c2: the row operators alone on the same 64 adapter copies (A as [32, 16, K]).
     x, slots, used = work.batch(64, 733)
     indptr, seg_slots, order = segments_of(slots.cpu().tolist())
@@ -643,11 +647,9 @@ def main() -> int:
         wanted = set(args.configs.split(",")) if args.configs != "all" else {"c1", "north_star", "c2", "c3", "c4", "c5", "dequant"}
         items, meta = [], {}
         if wanted & {"c1", "north_star", "c2"}:
-            it, me = decode_items(work, args.reps)
-            group = lambda name: name if name in ("c1", "c2") else "north_star"  # noqa: E731
-            keep = [i for i in it if group(i.name) in wanted]
-            items += keep
-            meta.update({i.name: me[i.name] for i in keep})
+            it, me = decode_items(work, args.reps, wanted)
+            items += it
+            meta.update(me)
         if "c3" in wanted:
             it, me = c3_items(device, args.reps)
             items += it
