@@ -160,10 +160,15 @@ int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_
 /* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);
  * y [m, N] bf16 with row stride y_stride; bias bf16 [N] or NULL;
  * lora NULL for the base linear alone. M <= 64 runs the decode kernel
- * (fp32 block scales required), M > 64 the prefill GEMM, which multiplies
- * the reference's dequantised weights bf16_rne(code * scale) bit for bit and
- * takes fp32 block scales or a double-quant state (rebuilt into the
- * workspace first; the workspace is then required even without LoRA).
+ * (fp32 block scales required). M > 64 runs either the prefill GEMM, which
+ * multiplies the reference's dequantised weights bf16_rne(code * scale) bit
+ * for bit and takes fp32 block scales or a double-quant state (rebuilt into
+ * the workspace first; the workspace is then required even without LoRA),
+ * or, when its 256 x 192 tiles would leave most CUs idle (few tokens, narrow
+ * N) and fp32 block scales are given, the decode kernel over 64-token chunks
+ * (one launch per chunk, in token order). A cost model of the two, from
+ * measured times, picks the plan; LF_PLAN_DECODE_CHUNKS or LF_PLAN_PREFILL
+ * forces one (a forced chunked plan needs fp32 block scales).
  * flags: LF_EXACT_WEIGHTS makes the decode kernel multiply the same exact
  * weights; by default it contracts bf16(code) and applies each fp32 block
  * scale to the block's MFMA sum. The prefill GEMM ignores the flag.
@@ -176,6 +181,8 @@ int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_
  * epilogue instead of a second launch). */
 #define LF_EXACT_WEIGHTS 1
 #define LF_SWIGLU_OUTPUT 2
+#define LF_PLAN_DECODE_CHUNKS 4
+#define LF_PLAN_PREFILL 8
 int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* weight,
                        const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                        void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);

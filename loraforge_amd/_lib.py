@@ -20,6 +20,8 @@ LF_EINVAL = 1
 LF_EHIP = 2
 LF_EXACT_WEIGHTS = 1
 LF_SWIGLU_OUTPUT = 2
+LF_PLAN_DECODE_CHUNKS = 4
+LF_PLAN_PREFILL = 8
 LF_TEST_WITHHOLD_PARTIALS = 0x100
 NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024
 ABI_VERSION = 1

@@ -1236,19 +1236,6 @@ void launch_tile(bool exact, bool lora, dim3 grid, hipStream_t s, const GemvPara
   else launch_exact<RT, XR, false>(exact, grid, s, p);
 }
 
-
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 struct GemvPlan {
   int rows;
   int row_groups;
@@ -1291,6 +1278,19 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
 
 int64_t gemv_workspace_bytes(int64_t, int64_t, int64_t, int, int) { return kWorkspaceHeader; }
 

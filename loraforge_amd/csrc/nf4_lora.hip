@@ -1,5 +1,9 @@
 // C-ABI entry of the fused NF4 + multi-LoRA linear: argument validation and
-// dispatch between the decode kernel (M <= 64 tokens) and the prefill GEMM.
+// dispatch between the decode kernel (M <= 64 tokens, or 64-token chunks of a
+// larger batch that the prefill tiles would not spread over the chip) and the
+// prefill GEMM.
+#include <algorithm>
+
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
 
@@ -12,7 +16,29 @@ int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                             void* workspace, int64_t workspace_bytes, bool withhold, void* stream);
+int device_cus();
 constexpr int64_t kDecodeMaxTokens = 64;
+
+// Whether M > 64 tokens are served faster by the decode kernel over 64-token
+// chunks than by one prefill launch. The prefill GEMM runs 256 x 192 tiles,
+// one workgroup per CU, so a call with fewer tiles than CUs leaves the rest
+// of the chip idle (c4: 256 tokens x 4096 features are 22 tiles on 256 CUs);
+// each decode chunk streams W again but uses every CU. Costs in us, from
+// measured times on MI355X: a decode launch of 64 tokens streams its weight
+// bytes (packed + fp32 scales) at about 0.8 TB/s, plus about 6 us with LoRA
+// (4096 x 4096: 11.9 us base only, 18.0 us with 32 rank-16 adapters); a
+// prefill round of tiles takes about 85 us per 4096 of K (c5: 1.81 rounds in
+// 189 us; c4: one round of 22 tiles in 77 us), plus about 20 us with LoRA.
+bool decode_chunks_cheaper(int64_t m, int64_t n, int64_t k, bool lora) {
+  const double weight_bytes = double(n) * double(k) * (0.5 + 4.0 / 64.0);
+  const double chunk_us = (lora ? 6.0 : 0.0) + weight_bytes / 0.8e6;
+  const int64_t chunks = (m + kDecodeMaxTokens - 1) / kDecodeMaxTokens;
+  const int64_t tiles = ((m + 255) / 256) * ((n + 191) / 192);
+  const int64_t cus = device_cus();
+  const int64_t rounds = (tiles + cus - 1) / cus;
+  const double prefill_us = double(rounds) * 85.0 * double(k) / 4096.0 + (lora ? 20.0 : 0.0);
+  return double(chunks) * chunk_us < prefill_us;
+}
 }  // namespace lf
 
 extern "C" int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices,
@@ -26,7 +52,11 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
                                   const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                                   void* workspace, int64_t workspace_bytes, int32_t flags, void* stream) {
   LF_REQUIRE(w != nullptr, "weight descriptor required");
-  LF_REQUIRE((flags & ~(LF_EXACT_WEIGHTS | LF_SWIGLU_OUTPUT | LF_TEST_WITHHOLD_PARTIALS)) == 0, "unknown flags");
+  LF_REQUIRE((flags & ~(LF_EXACT_WEIGHTS | LF_SWIGLU_OUTPUT | LF_PLAN_DECODE_CHUNKS | LF_PLAN_PREFILL |
+                        LF_TEST_WITHHOLD_PARTIALS)) == 0,
+             "unknown flags");
+  LF_REQUIRE((flags & (LF_PLAN_DECODE_CHUNKS | LF_PLAN_PREFILL)) != (LF_PLAN_DECODE_CHUNKS | LF_PLAN_PREFILL),
+             "LF_PLAN_DECODE_CHUNKS and LF_PLAN_PREFILL exclude each other");
   const bool withhold = (flags & LF_TEST_WITHHOLD_PARTIALS) != 0;
   const bool swiglu = (flags & LF_SWIGLU_OUTPUT) != 0;
   LF_REQUIRE(m >= 0 && m < (int64_t(1) << 31), "token count out of range");
@@ -51,17 +81,41 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
                "incomplete LoRA descriptor");
     LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
   }
+  const bool exact = (flags & LF_EXACT_WEIGHTS) != 0;
   if (m <= lf::kDecodeMaxTokens) {
     // The decode kernel streams fp32 block scales (as the reference serves
     // decode from prepare_scales output): nested states go through
     // lf_nf4_prepare_scales_dq once per weight.
     LF_REQUIRE(w->scales != nullptr,
                "decode (M <= 64) takes fp32 block scales: build them with lf_nf4_prepare_scales_dq");
-    return lf::launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
-                               (flags & LF_EXACT_WEIGHTS) != 0, swiglu, withhold, stream);
+    return lf::launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
+                               withhold, stream);
   }
-  return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, withhold,
-                                     stream);
+  bool chunked = false;
+  if (flags & LF_PLAN_DECODE_CHUNKS) {
+    LF_REQUIRE(w->scales != nullptr, "the chunked decode plan takes fp32 block scales");
+    chunked = true;
+  } else if (!(flags & LF_PLAN_PREFILL)) {
+    chunked = w->scales != nullptr && lf::decode_chunks_cheaper(m, n, k, lora != nullptr);
+  }
+  if (!chunked)
+    return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
+                                       withhold, stream);
+  // 64-token chunks in token order on the caller's stream; each is one decode
+  // launch over its rows of x, y and the token routes.
+  for (int64_t t0 = 0; t0 < m; t0 += lf::kDecodeMaxTokens) {
+    const int64_t mc = std::min<int64_t>(lf::kDecodeMaxTokens, m - t0);
+    lf_lora part{};
+    if (lora) {
+      part = *lora;
+      part.token_slots = lora->token_slots + t0;
+    }
+    const int rc = lf::launch_nf4_gemv(x + t0 * x_stride, mc, x_stride, w, bias, lora ? &part : nullptr,
+                                       y + t0 * y_stride, y_stride, workspace, workspace_bytes, exact, false,
+                                       withhold, stream);
+    if (rc != lf::kOk) return rc;
+  }
+  return lf::kOk;
 }
 
 extern "C" int lf_nf4_lora_status(const void* workspace, void* stream, int32_t* status) {

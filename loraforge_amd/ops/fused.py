@@ -126,17 +126,17 @@ def _workspace(device, stream: int, size: int, kind: str = "fused"):
         return ws
 
 
-def _kernel_takes_nested(m: int, exact: bool) -> bool:
+def _kernel_takes_nested(m: int, exact: bool, plan: str | None = None) -> bool:
     """Whether the call for ``m`` tokens passes a nested state to the library.
 
-    The decode kernel streams fp32 block scales, so decode calls take the
-    prepared scales, rebuilt once per weight and cached on the state. The
-    prefill launch rebuilds them itself into its workspace on every call;
-    by default prefill calls also take the cached scales (no per-call
-    rebuild), and ``exact=True`` passes the nested state (the results are
-    identical).
+    The decode kernel streams fp32 block scales, so decode calls (and the
+    chunked decode plan) take the prepared scales, rebuilt once per weight
+    and cached on the state. The prefill launch rebuilds them itself into its
+    workspace on every call; by default calls above 64 tokens also take the
+    cached scales (no per-call rebuild), and ``exact=True`` passes the nested
+    state, which keeps them on the prefill GEMM's exact weights.
     """
-    return m > 64 and exact
+    return m > 64 and exact and plan != "decode"
 
 
 def _version(tensor):
@@ -177,7 +177,7 @@ def _prepared_scales(qweight, state):
     return cached[1]
 
 
-def _weight_struct(qweight, state, scales, n, k, device, m=0, exact=False):
+def _weight_struct(qweight, state, scales, n, k, device, m=0, exact=False, plan=None):
     import torch
 
     code = state.code
@@ -191,7 +191,7 @@ def _weight_struct(qweight, state, scales, n, k, device, m=0, exact=False):
     keep = [qweight, code]
     if scales is None and not state.nested:
         scales = state.absmax
-    if scales is None and not _kernel_takes_nested(m, exact):
+    if scales is None and not _kernel_takes_nested(m, exact, plan):
         scales = _prepared_scales(qweight, state)
     if scales is not None:
         vector(scales.reshape(-1), "scales", torch.float32, device, n * k // 64)
@@ -271,6 +271,7 @@ def nf4_lora_linear(
     workspace=None,
     exact=False,
     swiglu=False,
+    plan=None,
 ):
     """``y = bf16(x @ dequant(W)^T) (+bias)``, then the per-token LoRA delta.
 
@@ -294,9 +295,16 @@ def nf4_lora_linear(
     LoRA-updated bf16 gate and up outputs. Batches of up to 32 tokens compute
     it in the decode kernel's epilogue (no gate/up round trip, no second
     launch); larger ones run the linear and then ``silu_mul``.
+
+    Above 64 tokens the library picks the prefill GEMM or the decode kernel
+    over 64-token chunks (when the prefill tiles would leave most of the chip
+    idle, e.g. 256 tokens x 4096 features); ``plan="prefill"`` or
+    ``plan="decode"`` forces one (``None``: the library's cost model).
     """
     import torch
 
+    if plan not in (None, "prefill", "decode"):
+        raise ValueError("plan must be None, 'prefill' or 'decode'")
     if not isinstance(x, torch.Tensor) or not isinstance(qweight, torch.Tensor):
         raise TypeError("x and qweight must be tensors")
     if state.quant_type != "nf4" or state.blocksize != 64:
@@ -336,7 +344,9 @@ def nf4_lora_linear(
 
             if out is not None and (out.dtype != torch.bfloat16 or out.shape != (*lead, width) or out.stride(-1) != 1):
                 raise ValueError("out must be bf16 [..., N/2] on the input device")
-            gate_up = nf4_lora_linear(x2, qweight, state, scales=scales, bias=bias, lora=lora, workspace=workspace, exact=exact)
+            gate_up = nf4_lora_linear(
+                x2, qweight, state, scales=scales, bias=bias, lora=lora, workspace=workspace, exact=exact, plan=plan
+            )
             h = silu_mul(gate_up, out=None if out is None else out.reshape(-1, width))
             return h.reshape(*lead, width) if out is None else out
     if out is None:
@@ -350,7 +360,7 @@ def nf4_lora_linear(
     if m == 0:
         return out
     require_arch(device)
-    w, keep = _weight_struct(qweight, state, scales, n, k, device, m, exact)
+    w, keep = _weight_struct(qweight, state, scales, n, k, device, m, exact, plan)
     lib = _lib.library()
     slices = lora.num_slices if lora is not None else 1
     max_rank = lora.max_rank if lora is not None else 1
@@ -376,7 +386,9 @@ def nf4_lora_linear(
                 y2.stride(0),
                 workspace.data_ptr(),
                 workspace.numel(),
-                (_lib.LF_EXACT_WEIGHTS if exact else 0) | (_lib.LF_SWIGLU_OUTPUT if swiglu else 0),
+                (_lib.LF_EXACT_WEIGHTS if exact else 0)
+                | (_lib.LF_SWIGLU_OUTPUT if swiglu else 0)
+                | {None: 0, "decode": _lib.LF_PLAN_DECODE_CHUNKS, "prefill": _lib.LF_PLAN_PREFILL}[plan],
                 stream,
             )
         )

@@ -48,6 +48,11 @@ def test_validation_errors_without_device_work():
     w = _lib.NF4Weight(n=100, k=64)
     with pytest.raises(ValueError, match="multiples of 64"):
         _lib.check(lib.lf_nf4_lora_linear(ctypes.c_void_p(16), 1, 64, ctypes.byref(w), None, None, ctypes.c_void_p(16), 64, None, 0, 0, None))
+    both = _lib.LF_PLAN_DECODE_CHUNKS | _lib.LF_PLAN_PREFILL
+    with pytest.raises(ValueError, match="exclude each other"):
+        _lib.check(lib.lf_nf4_lora_linear(ctypes.c_void_p(16), 100, 64, ctypes.byref(w), None, None, ctypes.c_void_p(16), 64, None, 0, both, None))
+    with pytest.raises(ValueError, match="unknown flags"):
+        _lib.check(lib.lf_nf4_lora_linear(ctypes.c_void_p(16), 100, 64, ctypes.byref(w), None, None, ctypes.c_void_p(16), 64, None, 0, 0x40, None))
 
 
 def test_workspace_size_is_host_arithmetic():

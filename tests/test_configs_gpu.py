@@ -123,8 +123,9 @@ def test_c3_swiglu_mlp(c3_mlp, m, device):
     workspace_clean(device)
 
 
-@pytest.mark.parametrize("m", [64, 256])
-def test_c4_retained_ranks_zipf_full_size(square_weight, m, device):
+@pytest.mark.parametrize("m,plan", [(64, None), (256, None), (256, "prefill")])
+def test_c4_retained_ranks_zipf_full_size(square_weight, m, plan, device):
+    """c4 at its full shape; 256 tokens run the chunked decode plan by default, the prefill GEMM when forced."""
     state, w_bits = square_weight
     rng = np.random.default_rng(737)
     ranks = rng.choice([4, 8, 16, 32, 64], size=128).tolist()
@@ -133,7 +134,7 @@ def test_c4_retained_ranks_zipf_full_size(square_weight, m, device):
     case["w_bits"] = w_bits
     x, q, st, lora, _ = to_device(case, device)
     assert lora.max_rank == 64
-    y = nf4_lora_linear(x, q, st, lora=lora)
+    y = nf4_lora_linear(x, q, st, lora=lora, plan=plan)
     torch.cuda.synchronize()
     close(bits(y), _cases.fused_expected(case))
     workspace_clean(device)

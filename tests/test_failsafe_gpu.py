@@ -40,18 +40,19 @@ def call(case, device, flags):
     return bits(y), status.value
 
 
-@pytest.mark.parametrize("m", [1, 7, 40, 64, 300])
-def test_withheld_producers_are_recomputed(m, device):
+@pytest.mark.parametrize("m,plan", [(1, 0), (7, 0), (40, 0), (64, 0), (300, "prefill"), (300, "decode")])
+def test_withheld_producers_are_recomputed(m, plan, device):
+    plan = {0: 0, "prefill": _lib.LF_PLAN_PREFILL, "decode": _lib.LF_PLAN_DECODE_CHUNKS}[plan]
     case = _cases.fused_case(m, 1024, 1024, ranks=(16, 8, 32, 4), seed=990 + m, bias=(m % 2 == 1),
                              null_frac=0.0)
     expect = _cases.fused_expected(case)
-    y, status = call(case, device, 0)
+    y, status = call(case, device, plan)
     assert status == 0
     close(y, expect)
-    y, status = call(case, device, _lib.LF_TEST_WITHHOLD_PARTIALS)
+    y, status = call(case, device, plan | _lib.LF_TEST_WITHHOLD_PARTIALS)
     assert status == 1
     close(y, expect)
-    y, status = call(case, device, 0)  # a fresh workspace after a give-up
+    y, status = call(case, device, plan)  # a fresh workspace after a give-up
     assert status == 0
     close(y, expect)
 
@@ -63,6 +64,6 @@ def test_withheld_producers_with_slices_and_many_adapters(device):
     routes = _cases.zipf_routes(rng, m, 48)
     case = _cases.fused_case(m, 1024, 512, ranks=[int(r) for r in rng.choice([4, 8, 16, 32], 48)], slices=2,
                              bounds=[0, 512, 1024], seed=13, token_slots=routes)
-    y, status = call(case, device, _lib.LF_TEST_WITHHOLD_PARTIALS)
+    y, status = call(case, device, _lib.LF_PLAN_PREFILL | _lib.LF_TEST_WITHHOLD_PARTIALS)
     assert status == 1
     close(y, _cases.fused_expected(case))

@@ -8,6 +8,8 @@ mixed ranks 0..64, all-base batches, counters left at zero, repeated calls,
 graph replay, and the prefill GEMM with segmented adapters.
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -180,7 +182,7 @@ def test_prefill_segments(m, dq, device):
     slots = np.repeat(np.array(seg_slots, np.int32), lengths)
     case = _cases.fused_case(m, 384, 512, ranks=(32, 4, 16), double_quant=dq, seed=m, token_slots=slots, bias=True)
     x, q, st, lora, bias = to_device(case, device)
-    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora)
+    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora, plan="prefill")
     torch.cuda.synchronize()
     close(bits(y), _cases.fused_expected(case))
     workspace_clean(device)
@@ -194,7 +196,7 @@ def test_prefill_short_and_odd_k(k, dq, device):
     slots = np.repeat(np.array([0, 1, -1], np.int32), [100, 150, 50])
     case = _cases.fused_case(m, 320, k, ranks=(8, 32), double_quant=dq, seed=k + dq, token_slots=slots)
     x, q, st, lora, _ = to_device(case, device)
-    y = nf4_lora_linear(x, q, st, lora=lora)
+    y = nf4_lora_linear(x, q, st, lora=lora, plan="prefill")
     torch.cuda.synchronize()
     close(bits(y), _cases.fused_expected(case))
 
@@ -206,7 +208,7 @@ def test_prefill_exact_weights(dq, device):
     slots = np.repeat(np.array([1, -1, 0], np.int32), [90, 30, 80])
     case = _cases.fused_case(m, 384, 512, ranks=(16, 8), double_quant=dq, seed=77, token_slots=slots, bias=True)
     x, q, st, lora, bias = to_device(case, device)
-    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora, exact=True)
+    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora, exact=True, plan="prefill")
     torch.cuda.synchronize()
     close(bits(y), _cases.fused_expected(case))
 
@@ -215,7 +217,7 @@ def test_prefill_slices_and_interleaved_routes(device):
     ranks = (8, 64, 0, 17)
     case = _cases.fused_case(300, 512, 256, ranks=ranks, slices=3, bounds=[0, 200, 448, 512], seed=5, null_frac=0.1)
     x, q, st, lora, _ = to_device(case, device)
-    y = nf4_lora_linear(x, q, st, lora=lora)
+    y = nf4_lora_linear(x, q, st, lora=lora, plan="prefill")
     torch.cuda.synchronize()
     close(bits(y), _cases.fused_expected(case))
 
@@ -229,7 +231,7 @@ def test_prefill_strided_output(offset, device):
     x, q, st, lora, bias = to_device(case, device)
     big = torch.full((m, n + 24), -7.0, dtype=torch.bfloat16, device=device)
     out = big[:, offset : offset + n]
-    nf4_lora_linear(x, q, st, bias=bias, lora=lora, out=out)
+    nf4_lora_linear(x, q, st, bias=bias, lora=lora, out=out, plan="prefill")
     torch.cuda.synchronize()
     close(bits(out), _cases.fused_expected(case))
     # Nothing outside the view was written.
@@ -245,17 +247,17 @@ def test_prefill_repeated_calls_and_graph_replay(device):
     expect = _cases.fused_expected(case)
     out = torch.empty(m, 448, dtype=torch.bfloat16, device=device)
     for _ in range(3):
-        nf4_lora_linear(x, q, st, lora=lora, out=out)
+        nf4_lora_linear(x, q, st, lora=lora, out=out, plan="prefill")
     torch.cuda.synchronize()
     close(bits(out), expect)
     eager = out.clone()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        nf4_lora_linear(x, q, st, lora=lora, out=out)
+        nf4_lora_linear(x, q, st, lora=lora, out=out, plan="prefill")
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
-            nf4_lora_linear(x, q, st, lora=lora, out=out)
+            nf4_lora_linear(x, q, st, lora=lora, out=out, plan="prefill")
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     for _ in range(4):
@@ -292,7 +294,7 @@ def test_decode_after_prefill_on_one_workspace(device):
     xp, qp, sp, lp, _ = to_device(pre, device)
     xd, qd, sd, ld, _ = to_device(dec, device)
     for call in range(1, 3):
-        yp = nf4_lora_linear(xp, qp, sp, lora=lp, workspace=ws)
+        yp = nf4_lora_linear(xp, qp, sp, lora=lp, workspace=ws, plan="prefill")
         yd = nf4_lora_linear(xd, qd, sd, lora=ld, workspace=ws)
         torch.cuda.synchronize()
         close(bits(yp), _cases.fused_expected(pre))
@@ -408,3 +410,55 @@ def test_prepared_scales_follow_in_place_weight_updates(device):
 
 def _dq_scales(st):
     return onf4.dq_scales(st["absmax_q"], st["absmax2"], st["code2"], st["offset"], dq_block=256)
+
+
+@pytest.mark.parametrize("m", [65, 130, 256, 300])
+@pytest.mark.parametrize("plan", [None, "decode", "prefill"])
+def test_plans_above_64_tokens(m, plan, device):
+    """Above 64 tokens both plans (decode over 64-token chunks, one prefill launch) match the oracle."""
+    case = _cases.fused_case(m, 1024, 1024, ranks=(16, 8, 32, 64, 4), seed=500 + m, bias=True)
+    x, q, st, lora, bias = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora, plan=plan)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+    if plan == "decode":
+        # Each chunk is exactly the decode call on its rows.
+        for t0 in range(0, m, 64):
+            rows = slice(t0, min(m, t0 + 64))
+            part = dataclasses.replace(lora, token_slots=lora.token_slots[rows])
+            yc = nf4_lora_linear(x[rows], q, st, bias=bias, lora=part)
+            assert torch.equal(yc, y[rows])
+    workspace_clean(device)
+
+
+def test_chunked_decode_graph_replay_and_strided_rows(device):
+    """The chunked plan's launches replay in a graph; strided x/y rows (views of wider tensors) are honoured."""
+    m, n, k = 200, 512, 1024
+    case = _cases.fused_case(m, n, k, ranks=(16, 32, 8), seed=61)
+    _, q, st, lora, _ = to_device(case, device)
+    xw = torch.zeros(m, k + 64, dtype=torch.bfloat16, device=device)
+    xw[:, :k] = t16(case["x"], device)
+    x = xw[:, :k]
+    big = torch.full((m, n + 40), -3.0, dtype=torch.bfloat16, device=device)
+    out = big[:, 8 : 8 + n]
+    expect = _cases.fused_expected(case)
+    nf4_lora_linear(x, q, st, lora=lora, out=out, plan="decode")
+    torch.cuda.synchronize()
+    close(bits(out), expect)
+    eager = out.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        nf4_lora_linear(x, q, st, lora=lora, out=out, plan="decode")  # the stream's workspace exists before capture
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            nf4_lora_linear(x, q, st, lora=lora, out=out, plan="decode")
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    assert torch.all(big[:, :8] == -3.0) and torch.all(big[:, 8 + n :] == -3.0)
