@@ -14,11 +14,12 @@
 // of slot g and every p-th group of 16 tokens routed to g (it finds them by
 // scanning the slot vector, 1024 entries at a time, with wave ballots). A
 // group is a 16 (A rows) x 16 (tokens) tile contracted over the whole K on
-// v_mfma_f32_16x16x32_bf16: the 16 waves of the workgroup take interleaved
-// 32-wide k steps, all of a wave's loads are issued before its first MFMA,
-// and the 16 partial tiles are summed through LDS in a fixed order, so the
-// result does not depend on timing. A of one slot is read from HBM once per
-// row tile; x rows come from L2.
+// v_mfma_f32_16x16x32_bf16: the four waves of the workgroup take interleaved
+// 32-wide k steps with eight steps of loads in flight each, and the partial
+// tiles are summed through LDS in a fixed order, so the result does not
+// depend on timing. A of one slot is read from HBM once per row tile; x rows
+// come from L2. For small token counts K is also split over workgroups
+// (tagged fp32 partials summed in chunk order by the last to arrive).
 // Expand: items (segment, 16 * 4 * waves output columns) on a persistent
 // grid. The segment's z rows are staged in LDS as bf16, zero past the rank;
 // each wave contracts 16-column tiles of B_g (A operand, one 16-byte row
