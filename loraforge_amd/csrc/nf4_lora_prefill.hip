@@ -919,6 +919,8 @@ namespace {
 int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 }  // namespace
 
+int device_cus();
+
 // Workspace: the control header (call epoch), the z flags (one per producer,
 // zparts per 256-token tile) at a fixed place (so a flag word only ever holds
 // tags, whatever the shapes of earlier calls on the workspace), the z rows
@@ -927,11 +929,21 @@ int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 constexpr int64_t kMaxFlags = kFlagRegion / 4;
 constexpr int kMaxZParts = 64;
 
-// z producers per M-tile: about 128 in all (a unit of 16 tokens of one
-// adapter each, when routing spreads), at most 64 per tile, and within the
-// flag region.
-int zparts_for(int64_t mtiles) {
-  return int(std::max<int64_t>(1, std::min<int64_t>({kMaxZParts, 128 / mtiles, kMaxFlags / mtiles})));
+// z producers per M-tile. Producers run first and hold a CU each (one
+// workgroup per CU), so they take CUs from the GEMM tiles, except where the
+// tiles' last round leaves CUs idle anyway: c5's 464 tiles on 256 CUs leave 48
+// idle in the second round, and 48 producers that start on those CUs delay no
+// tile, while 128 producers of one unit each (16 tokens) held half the CUs
+// for the first 22 us. So the producers fill the last round's slack (at most
+// 64 per tile, within the flag region), and never fall below 4 per tile, so
+// that no producer has more than a few units (each about 11 us at c5's
+// shape) to finish before its tile's consumers reach their epilogue.
+constexpr int kMinZParts = 4;
+int zparts_for(int64_t mtiles, int64_t tiles, int64_t cus) {
+  const int64_t rem = tiles % cus;
+  const int64_t slack = rem == 0 ? 0 : cus - rem;
+  const int64_t most = std::min<int64_t>(kMaxZParts, kMaxFlags / mtiles);
+  return int(std::max<int64_t>(1, std::min<int64_t>(most, std::max<int64_t>(kMinZParts, slack / mtiles))));
 }
 
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int) {
@@ -997,9 +1009,10 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   p.withhold = withhold ? 1 : 0;
   p.spin_limit = withhold ? 64 : (1 << 20);
   p.mtiles = int((m + wide::kBM - 1) / wide::kBM);
-  p.zparts = zparts_for(p.mtiles);
+  const int64_t tiles = p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN);
+  p.zparts = zparts_for(p.mtiles, tiles, device_cus());
   // LoRA launches put the z producers ahead of the GEMM tiles.
-  const dim3 grid(unsigned(p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN) + (lora ? p.mtiles * p.zparts : 0)));
+  const dim3 grid(unsigned(tiles + (lora ? p.mtiles * p.zparts : 0)));
   if (lora) hipLaunchKernelGGL((wide::gemm_kernel<true>), grid, dim3(wide::kThreads), 0, s, p);
   else hipLaunchKernelGGL((wide::gemm_kernel<false>), grid, dim3(wide::kThreads), 0, s, p);
   LF_HIP(hipGetLastError());
