@@ -21,7 +21,8 @@ benchmarks/check_qwen35_nf4_ops.py:11-41):
   c1          NF4 4096^2, B = 1, one rank-16 adapter;
   north_star  B = 1, 2, 4, ..., 64 (32 rank-16 adapters), also base only and
               with the exact-weights decode arithmetic;
-  c2          BF16 row_shrink + row_expand, 64 tokens, 32 x rank 16;
+  c2          BF16 row_shrink + row_expand, 64 tokens, 32 x rank 16 (c2_fused:
+              the same update by lora_apply in one launch);
   c3          NF4 + double-quant SwiGLU MLP 4096 / 12288 (gate/up, SwiGLU,
               down), 16 rank-8 adapters, B = 1 / 8 / 64; c3_fused_* runs the
               SwiGLU in the gate/up kernel's epilogue (two launches);
@@ -354,6 +355,18 @@ def decode_items(work: DecodeWorkload, reps: int, wanted=("c1", "north_star", "c
     c2_bytes = 262144 * used + 2 * 64 * work.k + 2 * 2 * 64 * work.n
     items.append(Timed("c2", [rows_call(layer) for layer in range(work.layers)], reps, c2_bytes))
     meta["c2"] = dict(batch=64, adapters_used=used, launches_per_call=2, segments=len(seg_slots))
+
+    # The same update in one launch (lora_apply: shrink + expand, z kept on chip).
+    from loraforge_amd.ops import lora_apply
+
+    y2 = y.clone()
+
+    def fused_call(layer):
+        batch = work.lora(layer, slots)
+        return lambda: lora_apply(x, y2, batch)
+
+    items.append(Timed("c2_fused", [fused_call(layer) for layer in range(work.layers)], reps, c2_bytes))
+    meta["c2_fused"] = dict(batch=64, adapters_used=used, launches_per_call=1, op="lora_apply")
     return items, meta
 
 

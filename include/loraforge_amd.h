@@ -187,6 +187,23 @@ int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride, const lf_
                        const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                        void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
 
+/* LoRA-only update of existing bf16 outputs, in one launch per 64 tokens:
+ * for every token t routed to slot g = token_slots[t] >= 0 with rank
+ * r = ranks[g] > 0, and every output column n of slice s,
+ *   z[t, s*r + j] = bf16(sum_w x[t, w] * A_g[s*r + j, w]),
+ *   y[t, n] = bf16(bf16(y[t, n]) + bf16(scales[g] * sum_j z[t, s*r + j] * B_g[n, j])).
+ * It replaces lf_row_shrink followed by lf_row_expand (the reference chain
+ * ops/lora_rows.py:51-239, ops/csrc/lora_rows.cu:35-162; its one-launch
+ * precedent is benchmarks/qwen35_tiny_fused.cu:34-53) when z is not needed
+ * by the caller: routing is per token (no segment lists) and z never leaves
+ * the chip. Tokens without an adapter keep their y bit for bit. x [m, K]
+ * bf16 (16-byte aligned rows, stride % 8 == 0), y [m, N] bf16 updated in
+ * place (row stride >= N); N and K multiples of 64; the workspace is that of
+ * lf_nf4_lora_linear for m <= 64 (lf_nf4_lora_workspace_size(min(m, 64), ...))
+ * and calls sharing it must not overlap. flags: LF_TEST_WITHHOLD_PARTIALS only. */
+int lf_lora_apply(const uint16_t* x, int64_t m, int64_t x_stride, int64_t n, int64_t k, const lf_lora* lora,
+                  uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
+
 /* Allocation-free variant of lf_nf4_lora_linear. It has no counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -125,6 +125,11 @@ _PROTOTYPES = {
             c_void_p,
         ],
     ),
+    "lf_lora_apply": (
+        ctypes.c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, ctypes.POINTER(Lora), c_void_p, c_int64, c_void_p, c_int64,
+         c_int32, c_void_p],
+    ),
     "lf_nf4_lora_status": (ctypes.c_int, [c_void_p, c_void_p, ctypes.POINTER(c_int32)]),
     "lf_swiglu": (ctypes.c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p]),
 }

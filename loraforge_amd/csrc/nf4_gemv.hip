@@ -951,7 +951,11 @@ __device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int
   }
 }
 
-template <int RT, int XR, bool kExact, bool kLora>
+// kResidual (with kLora): no weight. The base of each output is its current
+// value in y, which the call updates in place with the LoRA delta
+// (y = bf16(bf16(y) + bf16(scale * z B^T)), the row_shrink + row_expand chain
+// in one launch); no weight stream, no bias.
+template <int RT, int XR, bool kExact, bool kLora, bool kResidual = false>
 __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   using TL = Tile<RT, XR>;
   constexpr int TT = TL::kTT;
@@ -979,14 +983,15 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   const int nblk = p.k >> 6;
   const int kb0 = wave < kBase ? nblk * wave / kBase : 0;
   const int kend = wave < kBase ? nblk * (wave + 1) / kBase : 0;
-  const int nst = (kend - kb0 + TL::kSB - 1) / TL::kSB;
+  const int nst = kResidual ? 0 : (kend - kb0 + TL::kSB - 1) / TL::kSB;
   char* myring = ring + wave * D * TL::kStage;  // waves below kBase only
+  static_assert(!kResidual || (kLora && !kExact), "the residual form is a LoRA-only variant");
 
   // Codebook (and the LoRA slice bounds) through scalar loads: no vector
   // load may wait behind the copies.
   float cb[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) cb[i] = sload(p.code, i);
+  for (int i = 0; i < 16; ++i) cb[i] = kResidual ? 0.f : sload(p.code, i);
   int bounds[4] = {0, 0, 0, 0};
   if constexpr (kLora) {
 #pragma unroll
@@ -1011,7 +1016,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
       if (has0) first_frags(p, un0, wave, lane, pre);
     }
-    if constexpr (kLora) {
+    if constexpr (kLora && !kResidual) {
       // Workgroups that produce no unit hold their weight stream back by
       // about a microsecond (32 x 64 cycles), so the producers' unit
       // fragments are ahead of it in the memory queues (measured against no
@@ -1022,8 +1027,10 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       if (!has0) __builtin_amdgcn_s_sleep(32);
       else __builtin_amdgcn_s_sleep(16);
     }
+    if constexpr (!kResidual) {
 #pragma unroll
-    for (int s = 0; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, lo, hi, t0, mt, stage_kb(s), kend, lane);
+      for (int s = 0; s < D; ++s) issue_stage<TL>(p, myring + s * TL::kStage, lo, hi, t0, mt, stage_kb(s), kend, lane);
+    }
   } else if constexpr (kLora) {
     // The LoRA wave: the epoch and the first loads of its metadata chains
     // (vector loads: the barriers below wait only for scalar loads and LDS,
@@ -1033,6 +1040,19 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     g_tile = p.token_slots[t0 + min(lane, mt - 1)];
     const bool producer = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units;
     g_unit = producer ? p.token_slots[int(blockIdx.x) / p.kz] : -1;
+  }
+  // Residual form: the summing waves (one per 16 x 16 tile) fetch the outputs
+  // they will update now; nothing uses them before the end.
+  float yold[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (kResidual) {
+    if (wave < RT * TL::kTT) {
+      const int col = grow<TL>(lo, hi, (wave / TL::kTT) * 16 + (lane & 15));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = (wave % TL::kTT) * 16 + 4 * (lane >> 4) + e;
+        yold[e] = bf16_to_f32(p.y[int64_t(t0 + min(i, mt - 1)) * p.y_stride + col]);
+      }
+    }
   }
 
   if (threadIdx.x == 0) {
@@ -1088,7 +1108,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     // The unit's fragments were requested before the D stages: they have
     // landed once only the stages are outstanding.
     if (wave < kBase && has0) {
-      wait_vm<D * TL::kDma>();
+      wait_vm<kResidual ? 0 : D * TL::kDma>();
       first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
     }
   }
@@ -1186,8 +1206,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = t * 16 + 4 * g + e;  // tile token
-      float v = round_bf16(sum[e]);
-      if (p.bias) v = round_bf16(v + bias);
+      float v = kResidual ? yold[e] : round_bf16(sum[e]);
+      if (!kResidual && p.bias) v = round_bf16(v + bias);
       if constexpr (kLora) {
         if (i < mt && tm->g[i] >= 0) v += round_bf16(dsum[e] * tm->scale[i]);
       }
@@ -1231,8 +1251,9 @@ void launch_exact(bool exact, dim3 grid, hipStream_t s, const GemvParams& p) {
 }
 
 template <int RT, int XR>
-void launch_tile(bool exact, bool lora, dim3 grid, hipStream_t s, const GemvParams& p) {
-  if (lora) launch_exact<RT, XR, true>(exact, grid, s, p);
+void launch_tile(bool exact, bool lora, bool residual, dim3 grid, hipStream_t s, const GemvParams& p) {
+  if (residual) hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, true, true>), grid, dim3(kThreads), 0, s, p);
+  else if (lora) launch_exact<RT, XR, true>(exact, grid, s, p);
   else launch_exact<RT, XR, false>(exact, grid, s, p);
 }
 
@@ -1295,11 +1316,14 @@ int device_cus() {
 int64_t gemv_workspace_bytes(int64_t, int64_t, int64_t, int, int) { return kWorkspaceHeader; }
 
 // Fused NF4 + multi-LoRA linear for 1..64 tokens with fp32 block scales.
+// residual: no weight (only w->n and w->k are read) and a LoRA batch: y is
+// updated in place with each routed token's LoRA delta.
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
-                    bool exact, bool swiglu, bool withhold, void* stream) {
+                    bool exact, bool swiglu, bool withhold, void* stream, bool residual) {
   LF_REQUIRE(m >= 1 && m <= 64, "decode path handles 1..64 tokens");
-  LF_REQUIRE(w->scales != nullptr, "decode takes fp32 block scales (prepare double-quant scales first)");
+  LF_REQUIRE(residual || w->scales != nullptr, "decode takes fp32 block scales (prepare double-quant scales first)");
+  LF_REQUIRE(!residual || (lora && !bias && !swiglu && !exact), "the residual form takes a LoRA batch and nothing else");
   const GemvPlan pl = gemv_plan(m, w->n, w->k, device_cus(), lora ? lora->num_slices * lora->max_rank : 1);
   LF_REQUIRE(w->n % pl.rows == 0, "output width must be a multiple of %d", pl.rows);
   GemvParams p{};
@@ -1348,11 +1372,11 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   const dim3 grid(unsigned(pl.grid));
   auto s = static_cast<hipStream_t>(stream);
   const bool lo = lora != nullptr;
-  if (m <= 2) launch_tile<1, 2>(exact, lo, grid, s, p);
-  else if (m <= 8) launch_tile<1, 8>(exact, lo, grid, s, p);
-  else if (m <= 16) launch_tile<1, 16>(exact, lo, grid, s, p);
-  else if (m <= 32) launch_tile<1, 32>(exact, lo, grid, s, p);
-  else launch_tile<2, 32>(exact, lo, grid, s, p);
+  if (m <= 2) launch_tile<1, 2>(exact, lo, residual, grid, s, p);
+  else if (m <= 8) launch_tile<1, 8>(exact, lo, residual, grid, s, p);
+  else if (m <= 16) launch_tile<1, 16>(exact, lo, residual, grid, s, p);
+  else if (m <= 32) launch_tile<1, 32>(exact, lo, residual, grid, s, p);
+  else launch_tile<2, 32>(exact, lo, residual, grid, s, p);
   LF_HIP(hipGetLastError());
   return kOk;
 }

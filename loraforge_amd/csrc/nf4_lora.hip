@@ -11,7 +11,7 @@ namespace lf {
 int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
-                    bool exact, bool swiglu, bool withhold, void* stream);
+                    bool exact, bool swiglu, bool withhold, void* stream, bool residual = false);
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
@@ -123,5 +123,38 @@ extern "C" int lf_nf4_lora_status(const void* workspace, void* stream, int32_t* 
   auto s = static_cast<hipStream_t>(stream);
   LF_HIP(hipMemcpyAsync(status, static_cast<const char*>(workspace) + 8, 4, hipMemcpyDeviceToHost, s));
   LF_HIP(hipStreamSynchronize(s));
+  return lf::kOk;
+}
+
+extern "C" int lf_lora_apply(const uint16_t* x, int64_t m, int64_t x_stride, int64_t n, int64_t k, const lf_lora* lora,
+                             uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes, int32_t flags,
+                             void* stream) {
+  LF_REQUIRE((flags & ~LF_TEST_WITHHOLD_PARTIALS) == 0, "unknown flags");
+  LF_REQUIRE(m >= 0 && m < (int64_t(1) << 31), "token count out of range");
+  LF_REQUIRE(n > 0 && k > 0 && n % 64 == 0 && k % 64 == 0, "N and K must be positive multiples of 64");
+  LF_REQUIRE(n < (int64_t(1) << 28) && k < (int64_t(1) << 28), "shape too large");
+  if (m == 0) return lf::kOk;
+  LF_REQUIRE(x && y && lora, "null pointer argument");
+  LF_REQUIRE(lf::aligned16(x) && x_stride >= k && x_stride % 8 == 0, "x must be 16-byte aligned with row stride %% 8 == 0");
+  LF_REQUIRE(y_stride >= n, "output row stride must cover the output width");
+  LF_REQUIRE(lora->num_slices >= 1 && lora->num_slices <= 3, "num_slices must be in 1..3");
+  LF_REQUIRE(lora->max_rank >= 1 && lora->max_rank <= 64, "max_rank must be in 1..64");
+  LF_REQUIRE(lora->a_store && lora->a_offsets && lora->b_store && lora->b_offsets && lora->b_strides && lora->ranks &&
+                 lora->scales && lora->token_slots && lora->slice_offsets,
+             "incomplete LoRA descriptor");
+  LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
+  lf_nf4_weight shape{};
+  shape.n = n;
+  shape.k = k;
+  const bool withhold = (flags & LF_TEST_WITHHOLD_PARTIALS) != 0;
+  // One launch per 64 tokens, in token order.
+  for (int64_t t0 = 0; t0 < m; t0 += lf::kDecodeMaxTokens) {
+    const int64_t mc = std::min<int64_t>(lf::kDecodeMaxTokens, m - t0);
+    lf_lora part = *lora;
+    part.token_slots = lora->token_slots + t0;
+    const int rc = lf::launch_nf4_gemv(x + t0 * x_stride, mc, x_stride, &shape, nullptr, &part, y + t0 * y_stride,
+                                       y_stride, workspace, workspace_bytes, false, false, withhold, stream, true);
+    if (rc != lf::kOk) return rc;
+  }
   return lf::kOk;
 }

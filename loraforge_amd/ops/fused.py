@@ -396,6 +396,64 @@ def nf4_lora_linear(
     return out
 
 
+@ExperimentalAPI(reason="gfx950 one-launch row_shrink + row_expand; caller-owned device metadata.")
+def lora_apply(x, y, lora: LoraBatch, *, workspace=None):
+    """``y += LoRA(x)`` in place for every routed token, one launch per 64 tokens.
+
+    The reference chain ``row_shrink`` then ``row_expand``
+    (``ops/lora_rows.py:51-239``) without materialising z or building
+    segments: token ``t`` routed to slot ``g`` gets
+    ``y[t] = bf16(bf16(y[t]) + bf16(scale_g * bf16(x[t] A_g^T) B_g^T))`` per
+    slice, tokens without an adapter keep their bits. x: bf16 ``[M, K]``;
+    y: bf16 ``[M, N]`` (unit column stride); N and K multiples of 64. Runs on
+    the current stream with the cached per-stream workspace unless one is
+    passed. Returns ``y``.
+    """
+    import torch
+
+    if not isinstance(x, torch.Tensor) or not isinstance(y, torch.Tensor):
+        raise TypeError("x and y must be tensors")
+    if not isinstance(lora, LoraBatch):
+        raise TypeError("lora must be a LoraBatch")
+    device = x.device
+    if device.type != "cuda" or y.device != device:
+        raise ValueError("all tensors must be on the same CUDA/ROCm GPU")
+    if x.dtype != torch.bfloat16 or y.dtype != torch.bfloat16 or x.ndim != 2 or y.ndim != 2:
+        raise ValueError("x and y must be bf16 matrices")
+    if x.requires_grad or y.requires_grad:
+        raise ValueError("lora_apply is inference-only")
+    m, k = x.shape
+    n = y.shape[1]
+    if y.shape[0] != m:
+        raise ValueError("x and y must have the same number of rows (tokens)")
+    if n <= 0 or k <= 0 or n % 64 or k % 64:
+        raise ValueError("N and K must be positive multiples of 64")
+    if x.stride(1) != 1 or y.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        raise ValueError("x rows must be 16-byte aligned with a stride multiple of 8; unit column strides")
+    distinct_output(y, (x,))
+    if lora.slice_offsets.numel() - 1 != lora.num_slices:
+        raise ValueError("slice_offsets length disagrees with num_slices")
+    if m == 0:
+        return y
+    require_arch(device)
+    lstruct = _lora_struct(lora, m, k, n, device)
+    lib = _lib.library()
+    with torch.cuda.device(device):
+        stream = _lib.stream_of(device)
+        need = workspace_bytes(min(m, 64), n, k, num_slices=lora.num_slices, max_rank=lora.max_rank)
+        if workspace is None:
+            workspace = _workspace(device, stream, need)
+        elif workspace.dtype != torch.uint8 or workspace.device != device or workspace.numel() < need:
+            raise ValueError(f"workspace must be uint8 on the input device with at least {need} bytes")
+        _lib.check(
+            lib.lf_lora_apply(
+                x.data_ptr(), m, x.stride(0), n, k, lstruct, y.data_ptr(), y.stride(0),
+                workspace.data_ptr(), workspace.numel(), 0, stream,
+            )
+        )
+    return y
+
+
 def decode_status(workspace=None, device=None) -> int:
     """Status word of the fused calls on a workspace (0 = ok; 1 = a wait for z gave up); synchronises."""
     import ctypes
