@@ -493,11 +493,17 @@ def c4_items(device, reps: int, copies: int = 8):
         a = (torch.randn(total_a, generator=g) * 0.02).bfloat16().to(device)
         b = (torch.randn(total_b, generator=g) * 0.02).bfloat16().to(device)
         lora = LoraBatch(a_store=a, b_store=b, max_rank=64, **meta_t)
-        calls.append(lambda q=q, st=st, lora=lora: nf4_lora_linear(x, q, st, lora=lora, out=out))
+        calls.append((q, st, lora))
     work = n * k // 2 + n * k // 16 + int(sum(16384 * int(ranks[i]) for i in used)) + tokens * k * 2 * 2
     flops = 2 * tokens * n * k + int(sum(2 * int((routes == i).sum()) * int(ranks[i]) * (k + n) for i in used))
-    item = Timed("c4", calls, reps, work)
-    return [item], {"c4": dict(tokens=tokens, adapters_used=int(used.size), flops_per_call=flops, path="prefill (M > 64)")}
+
+    def thunks(plan):
+        return [lambda q=q, st=st, lora=lora: nf4_lora_linear(x, q, st, lora=lora, out=out, plan=plan) for q, st, lora in calls]
+
+    # The library's plan (the chunked decode at this shape) and the prefill GEMM forced, on the same copies.
+    items = [Timed("c4", thunks(None), reps, work), Timed("c4_prefill", thunks("prefill"), reps, work)]
+    info = dict(tokens=tokens, adapters_used=int(used.size), flops_per_call=flops)
+    return items, {"c4": dict(info, plan="library choice"), "c4_prefill": dict(info, plan="prefill GEMM (forced)")}
 
 
 def c5_items(device, reps: int):

@@ -778,7 +778,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       return d;
     };
     const int first = next_live(-1);
-    uint4 cb0[kJ], cb1[kJ], nb0[kJ], nb1[kJ];  // B of the slot being applied and of the next one
+    // B of the slot being applied (index 0) and of the next kAhead live slots,
+    // requested that far ahead: with dozens of slots in a tile (retained-rank
+    // batches under Zipf routing) each slot would otherwise cost one memory
+    // round trip.
+    constexpr int kAhead = 2;
+    int dq[kAhead + 1];
+    uint4 bq0[kAhead + 1][kJ], bq1[kAhead + 1][kJ];
     wait_z(p, mt, tag, tslot, list, order, mrank, mstride, mscale, mboff, reinterpret_cast<float*>(xring), zmissing);
     uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle (the ring is idle)
     for (int s = 0; s < p.slices; ++s) {
@@ -789,7 +795,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       // for slice 0 the first slot's B, requested before the base rounding.
       load_zs(s);
       if (s == 0) {
-        if (first < nd) request_b(first, cb0, cb1);
+        if (first < nd) request_b(first, bq0[0], bq1[0]);
         round_bias(p, acc, wn0, g);
       }
       wait_vm<0>();  // the z loads (and anything requested after them)
@@ -805,20 +811,25 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       const bool inside = lo <= wn0 && wn0 + 48 <= hi;
       // delta[n][m] = sum_j B_g[n][j] z[m][j] for the wave's 128 tokens x 48
       // features, added with the reference's two roundings to the tokens
-      // routed to g and the features of slice s. The next slot's B is
-      // requested before this slot's MFMAs, so its latency is hidden.
-      if (s > 0 && first < nd) request_b(first, cb0, cb1);
-      for (int d = first; d < nd;) {
-        const int dn = next_live(d);
-        if (dn < nd) request_b(dn, nb0, nb1);
+      // routed to g and the features of slice s. The B of the next kAhead
+      // live slots is in flight while this slot's MFMAs run.
+      if (s > 0 && first < nd) request_b(first, bq0[0], bq1[0]);
+      dq[0] = first;
+#pragma unroll
+      for (int a = 1; a <= kAhead; ++a) {
+        dq[a] = dq[a - 1] < nd ? next_live(dq[a - 1]) : nd;
+        if (dq[a] < nd) request_b(dq[a], bq0[a], bq1[a]);
+      }
+      while (dq[0] < nd) {
+        const int d = dq[0];
         const int gd = list[d];
         const bool two = mrank[d] > 32;
         const float scale = mscale[d];
         bf16x8 l0[kJ], l1[kJ];
 #pragma unroll
         for (int j = 0; j < kJ; ++j) {
-          l0[j] = b_frag(cb0[j], d, g * 8, j);
-          l1[j] = two ? b_frag(cb1[j], d, 32 + g * 8, j) : as_bf16x8(make_uint4(0, 0, 0, 0));
+          l0[j] = b_frag(bq0[0][j], d, g * 8, j);
+          l1[j] = two ? b_frag(bq1[0][j], d, 32 + g * 8, j) : as_bf16x8(make_uint4(0, 0, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -845,12 +856,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
             }
           }
         }
-        d = dn;
+        // Rotate, then request the slot kAhead places on.
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-          cb0[j] = nb0[j];
-          cb1[j] = nb1[j];
+        for (int a = 0; a < kAhead; ++a) {
+          dq[a] = dq[a + 1];
+#pragma unroll
+          for (int j = 0; j < kJ; ++j) {
+            bq0[a][j] = bq0[a + 1][j];
+            bq1[a][j] = bq1[a + 1][j];
+          }
         }
+        dq[kAhead] = dq[kAhead - 1] < nd ? next_live(dq[kAhead - 1]) : nd;
+        if (dq[kAhead] < nd) request_b(dq[kAhead], bq0[kAhead], bq1[kAhead]);
       }
     }
   } else {
