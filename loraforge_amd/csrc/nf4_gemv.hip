@@ -93,8 +93,11 @@ struct GemvParams {
   int slices;
   int max_rank;
   int zw;         // z row width: slices * max_rank
-  int units;      // shrink units: m * kz (unit u = token u / kz, k-slice u % kz)
+  int units;      // shrink units: m * usplit * kz
   int kz;         // k-slices per token
+  int usplit;     // row ranges per token (unit u: token u / (usplit * kz), range (u / kz) % usplit, k-slice u % kz)
+  int urows;      // A rows per range (a multiple of 16)
+  uint32_t unit_inv;  // ceil(2^21 / (usplit * kz)): u / (usplit * kz) by a multiply (u <= 1024)
   int kz_len;     // k per slice (multiple of 64)
   int producers;  // workgroups b < producers make units b, b + producers, ...
   int* status;    // set to 1 when a bounded wait for partials gave up (they were then recomputed)
@@ -229,10 +232,12 @@ __device__ __forceinline__ void contract(const Frags<TL>& f, int kb, int kend, f
 // ---------------------------------------------------------------------------
 // LoRA (the last wave of every workgroup is the LoRA wave).
 //
-// Shrink: unit u = (token t = u / kz, k-slice u % kz) is computed early in
-// workgroup u % producers: all eight waves contract x[t] with the slices * r
-// rows of the token's adapter A_g over the slice (MFMA, the token row
-// repeated across the 16 MFMA rows); the LoRA wave sums their partial rows
+// Shrink: unit u = (token t, row range, k-slice) is computed early in
+// workgroup u % producers: the contraction waves contract x[t] with the
+// range's rows (up to urows of the slices * r rows of the token's adapter
+// A_g) over the slice (MFMA, the token in row 0); a token of high rank is
+// split over several units so that no producer streams a whole rank-64 A
+// while the others wait; the LoRA wave sums their partial rows
 // and stores zp[u][j] with device-scope 64-bit stores, each value paired
 // with the call's tag. The fragments of a workgroup's first unit are
 // requested between its first and second weight stages, so they are not
@@ -263,24 +268,34 @@ __device__ __forceinline__ uint64_t tagged_load(const uint64_t* p) {
 struct Unit {
   int t;      // token
   int ks;     // k-slice
-  int rows;   // slices * rank
+  int j0;     // first A row of the unit's range
+  int rows;   // rows of the range (slices * rank - j0, at most urows)
   int kb;     // first k of the slice
   int steps;  // 32-k MFMA steps in the slice
   int64_t aoff;
 };
 
+// Token of unit u (u < 1024; the rounding error of the multiply stays below
+// 1024 / 2^21 < 1 / (usplit * kz)).
+__device__ __forceinline__ int unit_token(const GemvParams& p, int u) { return int((uint32_t(u) * p.unit_inv) >> 21); }
+
 // Unit u's token, adapter rows and k-slice (scalar loads); false when the
-// token has no adapter (base only), so nothing is produced.
-// g: the token's slot, token_slots[u / kz], loaded by the caller.
+// token has no adapter (base only) or its rows end before the unit's range,
+// so nothing is produced.
+// g: the token's slot, token_slots[unit_token(p, u)], loaded by the caller.
 __device__ __forceinline__ bool unit_of_slot(const GemvParams& p, int u, int g, Unit& un) {
-  un.t = u / p.kz;
-  un.ks = u - un.t * p.kz;
+  un.t = unit_token(p, u);
+  const int rest = u - un.t * p.usplit * p.kz;
+  const int range = rest >> (31 - __builtin_clz(p.kz));  // kz is a power of two
+  un.ks = rest - range * p.kz;
   const int ks = un.ks;
   if (g < 0) return false;
   const int r = sload(p.ranks, g);
   if (r <= 0 || r > p.max_rank) return false;
-  un.aoff = sload(p.a_offsets, g);
-  un.rows = p.slices * r;
+  un.j0 = range * p.urows;
+  if (un.j0 >= p.slices * r) return false;
+  un.aoff = sload(p.a_offsets, g) + int64_t(un.j0) * p.k;
+  un.rows = min(p.urows, p.slices * r - un.j0);
   un.kb = ks * p.kz_len;
   un.steps = (min(p.k, un.kb + p.kz_len) - un.kb) >> 5;
   if (un.steps <= 0) {  // an empty trailing slice: zero partials, read at k = 0
@@ -291,13 +306,14 @@ __device__ __forceinline__ bool unit_of_slot(const GemvParams& p, int u, int g, 
 }
 
 __device__ __forceinline__ bool unit_of(const GemvParams& p, int u, Unit& un) {
-  return unit_of_slot(p, u, sload(p.token_slots, u / p.kz), un);
+  return unit_of_slot(p, u, sload(p.token_slots, unit_token(p, u)), un);
 }
 
-// Partial of value j of unit (token t, k-slice ks): entry (t * zw + j) * kz +
-// ks, so the kz partials a consumer sums for one value are adjacent.
+// Partial of row j of a unit's range (value j0 + j of token t, k-slice ks):
+// entry (t * zw + j0 + j) * kz + ks, so the kz partials a consumer sums for
+// one value are adjacent.
 __device__ __forceinline__ int64_t partial_index(const GemvParams& p, const Unit& un, int j) {
-  return (int64_t(un.t) * p.zw + j) * p.kz + un.ks;
+  return (int64_t(un.t) * p.zw + un.j0 + j) * p.kz + un.ks;
 }
 
 // x and A fragments of the MFMA steps st0 + i * stride (i < kBatch) of rows
@@ -1039,7 +1055,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
     epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     g_tile = p.token_slots[t0 + min(lane, mt - 1)];
     const bool producer = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units;
-    g_unit = producer ? p.token_slots[int(blockIdx.x) / p.kz] : -1;
+    g_unit = producer ? p.token_slots[unit_token(p, int(blockIdx.x))] : -1;
   }
   // Residual form: the summing waves (one per 16 x 16 tile) fetch the outputs
   // they will update now; nothing uses them before the end.
@@ -1263,6 +1279,8 @@ struct GemvPlan {
   int grid;
   int kz;
   int kz_len;
+  int usplit;
+  int urows;
   int units;
   int producers;
 };
@@ -1293,7 +1311,14 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
   pl.kz = int(kz);  // trailing slices may be empty (their partials are zero)
   // The consumer holds 16 entries per lane and batch: one token's kz * zw
   // entries must fit 1024 (kz > 1 only when that holds; zw <= 192 at kz = 1).
-  pl.units = int(m) * pl.kz;
+  // Tokens of wide z (high ranks, several slices) split their rows over as
+  // many units as the producers allow: a rank-64 token's whole A (512 KB at
+  // K = 4096) in one workgroup held every consumer for about 30 us.
+  const int64_t groups = (zw + 15) / 16;  // 16-row groups per token
+  const int64_t split = std::max<int64_t>(1, std::min<int64_t>(groups, cap / (m * kz)));
+  pl.urows = int((groups + split - 1) / split) * 16;
+  pl.usplit = int((groups * 16 + pl.urows - 1) / pl.urows);
+  pl.units = int(m) * pl.usplit * pl.kz;
   pl.producers = int(cap);
   return pl;
 }
@@ -1343,7 +1368,7 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   if (lora) {
     LF_REQUIRE(workspace && workspace_bytes >= kWorkspaceHeader, "workspace too small: need %lld bytes",
                (long long)kWorkspaceHeader);
-    LF_REQUIRE(kPartialsOffset + int64_t(pl.units) * lora->num_slices * lora->max_rank * 8 <= kWorkspaceHeader,
+    LF_REQUIRE(kPartialsOffset + m * pl.kz * lora->num_slices * lora->max_rank * 8 <= kWorkspaceHeader,
                "shrink partials exceed the control header");
     LF_REQUIRE(aligned16(workspace), "workspace must be 16-byte aligned");
     p.a_store = lora->a_store;
@@ -1360,6 +1385,10 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
     p.zw = lora->num_slices * lora->max_rank;
     p.units = pl.units;
     p.kz = pl.kz;
+    p.usplit = pl.usplit;
+    p.urows = pl.urows;
+    p.unit_inv = ((1u << 21) + uint32_t(pl.usplit * pl.kz) - 1) / uint32_t(pl.usplit * pl.kz);
+    LF_REQUIRE(pl.units <= 1024, "too many shrink units");
     p.kz_len = pl.kz_len;
     p.producers = pl.producers;
     char* ws = static_cast<char*>(workspace);
