@@ -530,6 +530,7 @@ struct TileMeta {
   int dr[32];
   int dstride[32];
   int64_t dboff[32];
+  int start[33];  // z values the tile's tokens need (slices * r, 0 base only), exclusive prefix; start[32] = total
   int nd;
   int ready;  // set once the fields above are written (cleared at launch start)
 };
@@ -635,9 +636,20 @@ __device__ __forceinline__ TokenMeta token_meta(const GemvParams& p, int g, int 
 // The LoRA wave, part 1b (after the table barrier): tile metadata and
 // distinct slots into LDS, then the ready flag.
 template <class TL>
-__device__ void lora_meta(char* lds, const TokenMeta& m, int lane) {
+__device__ void lora_meta(char* lds, const TokenMeta& m, int slices, int lane) {
   TileMeta* tm = reinterpret_cast<TileMeta*>(lds + LoraLds<TL>::kMeta);
   const int g = m.g, r = m.r, stride = m.stride;
+  // Where each token's z values start in the tile's compact list of needed
+  // values (a shuffle scan over the 32 token lanes).
+  const int cnt = (lane < 32 && g >= 0) ? slices * r : 0;
+  int incl = cnt;
+#pragma unroll
+  for (int d = 1; d < 32; d <<= 1) {
+    const int v = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += v;
+  }
+  if (lane < 32) tm->start[lane] = incl - cnt;
+  if (lane == 31) tm->start[32] = incl;
   const float scale = m.scale;
   const int64_t boff = m.boff;
   if (lane < 32) {
@@ -667,19 +679,17 @@ __device__ void lora_meta(char* lds, const TokenMeta& m, int lane) {
   if (lane == 0) *(volatile __attribute__((address_space(3))) int*)(&tm->ready) = 1;
 }
 
-// a / d for 0 <= a, d <= 1024 through a multiply: inverse = ceil(2^21 / d);
-// the rounding error stays below 1024 / 2^21 < 1 / 1024 <= 1 - frac(a / d).
-__device__ __forceinline__ uint32_t small_inverse(int d) { return ((1u << 21) + uint32_t(d) - 1) / uint32_t(d); }
-__device__ __forceinline__ int small_div(int a, uint32_t inverse) { return int((uint32_t(a) * inverse) >> 21); }
 
-// The LoRA wave, part 2: z of the tile. The tile's partials are one
-// contiguous block: token i's value j has its KZ k-slice partials at
-// ((t0 + i) * zw + j) * KZ .. + KZ. Each lane owns up to 16 / KZ values of a
-// batch of whole tokens; the entries a routed token needs (j < slices * r)
-// are polled until all carry the call's tag, then each value is summed in
-// registers, z[i][j] = bf16(sum), and stored slice padded into LDS (zero past
-// the rank). Entries of base-only tokens and past the rank are never waited
-// for or used. KZ (k-slices per token) is a power of two up to 16.
+// The LoRA wave, part 2: z of the tile. Token i's value j has its KZ
+// k-slice partials at ((t0 + i) * zw + j) * KZ .. + KZ. Only the values the
+// routed tokens need (j < slices * r) are read: they are numbered in a
+// compact list (token i's at start[i] .. start[i + 1]), each lane owns up to
+// 16 / KZ of a batch of that list (its token found by a binary search over
+// start), polls them until all carry the call's tag, sums each value in
+// registers, z[i][j] = bf16(sum), and stores it slice padded into LDS (zero
+// past the rank). A tile of 32 rank-64 tokens needs 2048 values, two
+// batches; one whose ranks average 25 needs one. KZ (k-slices per token) is
+// a power of two up to 16.
 // z value j of token t (slot g) before rounding: sum over K of
 // x[t][k] * A_g[j][k] (A rows packed at s * r, so value j is row j), in fp32.
 __device__ __forceinline__ float full_dot(const GemvParams& p, int t, int g, int j) {
@@ -707,20 +717,23 @@ __device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + L::kMeta);
   uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
   for (int e = lane; e < TL::kXR * 192 / 8; e += 64) reinterpret_cast<uint4*>(zl)[e] = make_uint4(0, 0, 0, 0);
-  const int tpb = max(1, (64 * kOut) / p.zw);  // whole tokens per batch (zw <= 192)
-  const uint32_t inv_zw = small_inverse(p.zw);
-  for (int i0 = 0; i0 < mt; i0 += tpb) {
-    const int nout = min(tpb, mt - i0) * p.zw;  // values in this batch
-    const uint64_t* block = p.zp + (int64_t(t0 + i0) * p.zw) * KZ;
+  const int total = tm->start[32];
+  for (int o0 = 0; o0 < total; o0 += 64 * kOut) {
+    const uint64_t* block = p.zp + int64_t(t0) * p.zw * KZ;
     int il[kOut], jv[kOut];
     bool need[kOut];
 #pragma unroll
     for (int q = 0; q < kOut; ++q) {
-      const int o = min(q * 64 + lane, nout - 1);
-      il[q] = small_div(o, inv_zw);
-      jv[q] = o - il[q] * p.zw;
-      const int i = i0 + il[q];
-      need[q] = q * 64 + lane < nout && tm->g[i] >= 0 && jv[q] < p.slices * tm->r[i];
+      const int o = min(o0 + q * 64 + lane, total - 1);
+      // The last token whose values start at or before o (tokens with none
+      // share their successor's start and are passed over).
+      int i = 0;
+#pragma unroll
+      for (int step = 16; step > 0; step >>= 1)
+        if (tm->start[i + step] <= o) i += step;
+      il[q] = i;
+      jv[q] = o - tm->start[i];
+      need[q] = o0 + q * 64 + lane < total;
     }
     uint64_t v[kOut][KZ];
     bool gave_up = false;
@@ -729,7 +742,7 @@ __device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
       for (int q = 0; q < kOut; ++q)
 #pragma unroll
         for (int ks = 0; ks < KZ; ++ks)  // unconditional: no per-load branch
-          v[q][ks] = tagged_load(block + int64_t(min(q * 64 + lane, nout - 1)) * KZ + ks);
+          v[q][ks] = tagged_load(block + (int64_t(il[q]) * p.zw + jv[q]) * KZ + ks);
       bool ok = true;
 #pragma unroll
       for (int q = 0; q < kOut; ++q)
@@ -747,7 +760,7 @@ __device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
       float z = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KZ; ++ks) z += __uint_as_float(uint32_t(v[q][ks]));
-      const int i = i0 + il[q];
+      const int i = il[q];
       const int j = jv[q];
       const int ri = tm->r[i];
       const int s = int(j >= ri) + int(j >= 2 * ri) + int(j >= 3 * ri);  // slice of value j (3: past them)
@@ -1099,7 +1112,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       tmeta = token_meta(p, g_tile, mt, lane);
       has0 = g_unit >= 0 && unit_of_slot(p, blockIdx.x, __builtin_amdgcn_readfirstlane(g_unit), un0);
       const uint32_t tag = __builtin_amdgcn_readfirstlane(epoch) + 1u;
-      lora_meta<TL>(lora_lds, tmeta, lane);
+      lora_meta<TL>(lora_lds, tmeta, p.slices, lane);
       if (has0) publish_first_unit(p, red, &prod_done, un0, tag, lane);
       produce_other_units(p, tag, lane);
     }
