@@ -18,6 +18,9 @@ tests do with ``SimpleNamespace``):
   ``weight_indices[s]``;
 * ``scalings[slot]`` is the slot's LoRA scaling.
 
+``apply_lora`` does the same for a projection whose base output the caller
+already holds (y updated in place by ``lora_apply``).
+
 The per-token slot map is built on the device with a few tensor kernels and
 no read-back (``num_segments`` is the host count SGLang keeps; under graph
 capture it is a constant of the captured batch), into a caller-owned
@@ -26,7 +29,7 @@ buffer when one is given, so a captured graph keeps its address.
 
 from __future__ import annotations
 
-from ..ops.fused import LoraBatch, nf4_lora_linear
+from ..ops.fused import LoraBatch, lora_apply, nf4_lora_linear
 
 
 def token_slots_from_batch_info(info, tokens: int, *, out=None):
@@ -93,3 +96,15 @@ def apply_nf4_lora(x, qweight, state, info, table, *, bias=None, out=None, token
     """y = NF4 base linear + every token's LoRA for SGLang's batch, in one launch."""
     lora = lora_batch_from_batch_info(info, table, tokens=x.shape[0], token_slots=token_slots, slice_offsets=slice_offsets)
     return nf4_lora_linear(x, qweight, state, bias=bias, lora=lora, out=out)
+
+
+def apply_lora(x, y, info, table, *, token_slots=None, slice_offsets=None):
+    """``y += LoRA(x)`` in place for SGLang's batch, one launch per 64 tokens.
+
+    For projections whose base output SGLang computes itself (unquantised
+    layers): the Fleet backend's A pass then B pass over ``batch_info``
+    (``integrations/_sglang_fleet.py:271-407``) as one ``lora_apply`` call on
+    the same slot map.
+    """
+    lora = lora_batch_from_batch_info(info, table, tokens=x.shape[0], token_slots=token_slots, slice_offsets=slice_offsets)
+    return lora_apply(x, y, lora)

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from loraforge_amd.integrations import apply_nf4_lora, lora_batch_from_batch_info
+from loraforge_amd.integrations import apply_lora, apply_nf4_lora, lora_batch_from_batch_info
 from loraforge_amd.runtime import AdapterTable, RetainedLayout
 from oracle import linear
 from oracle import nf4 as onf4
@@ -111,3 +111,27 @@ def test_bridge_graph_replay_follows_new_metadata(weight, device):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(slots_buf.cpu().numpy(), routes)
         close(bits(out), expected(x_bits, w_bits, batch, routes, 1024))
+
+
+@pytest.mark.parametrize("tokens", [5, 64, 150])
+def test_bridge_lora_only_update(tokens, device):
+    """apply_lora: SGLang's batch over a retained layout, y (the caller's base output) updated in place."""
+    rng = np.random.default_rng(200 + tokens)
+    layout = retained_pool(rng, device)
+    info, routes = random_info(rng, tokens, 6, padded=2, device=device)
+    info.scalings = torch.tensor([2.0, 1.0, 0.5, 1.5, 0.25, 1.0], device=device)
+    x_bits = _cases.bf16(rng.standard_normal((tokens, 512)))
+    y_bits = _cases.bf16(rng.standard_normal((tokens, 1024)))
+    y = t16(y_bits, device)
+    apply_lora(t16(x_bits, device), y, info, layout)
+    torch.cuda.synchronize()
+    batch = lora_batch_from_batch_info(info, layout, tokens=tokens)
+    as_np = lambda t: t.cpu().numpy()  # noqa: E731
+    want = linear.lora_apply(
+        x_bits, y_bits, a_store=bits(batch.a_store), a_offsets=as_np(batch.a_offsets), b_store=bits(batch.b_store),
+        b_offsets=as_np(batch.b_offsets), b_strides=as_np(batch.b_strides), ranks=as_np(batch.ranks),
+        scales=as_np(batch.scales), token_slots=routes, slice_offsets=as_np(batch.slice_offsets), n_total=1024,
+    )
+    close(bits(y), want)
+    idle = routes < 0
+    assert np.array_equal(bits(y)[idle], y_bits[idle])
