@@ -325,7 +325,6 @@ struct UnitFragsN {
   u32x4 xv[NB];
   u32x4 av[NB];
 };
-using UnitFrags = UnitFragsN<kBatch>;
 
 // A 16-byte global load the compiler does not track. While direct LDS copies
 // are in flight, the compiler waits for every outstanding memory operation
@@ -378,28 +377,31 @@ __device__ __forceinline__ void unit_frags(const GemvParams& p, const Unit& un, 
 }
 
 // The first batch of a workgroup's first unit, requested in the prologue
-// (untracked loads). x is compact: lane 4 i + g (i < kBatch, g < 4) holds
+// (untracked loads). x is compact: lane 4 i + g (i < NB <= 16, g < 4) holds
 // the 16 bytes of k-group g of step st0 + i * kProd, one gathered load; the
 // MFMA layout (row 0 only) is formed when used.
-struct FirstFrags {
+template <int NB>
+struct FirstFragsN {
+  static_assert(NB <= 16, "one compact x register");
   u32x4 xc;
-  u32x4 av[kBatch];
+  u32x4 av[NB];
 };
 
-__device__ __forceinline__ void first_frags(const GemvParams& p, const Unit& un, int st0, int lane, FirstFrags& f) {
+template <int NB>
+__device__ __forceinline__ void first_frags(const GemvParams& p, const Unit& un, int st0, int lane, FirstFragsN<NB>& f) {
   const int jn = lane & 15;
   const int kg = lane >> 4;
   {
-    const int i = min(lane >> 2, kBatch - 1);
+    const int i = min(lane >> 2, NB - 1);
     const int st = st0 + i * kProd;
     const int sc = st < un.steps ? st : max(un.steps - 1, 0);
     const uint16_t* xp = p.x + int64_t(un.t) * p.x_stride + un.kb + 32 * sc + 8 * (lane & 3);
-    f.xc = global_load128_untracked_masked(xp, (uint64_t(1) << (4 * kBatch)) - 1);
+    f.xc = global_load128_untracked_masked(xp, NB == 16 ? ~0ull : (uint64_t(1) << (4 * NB)) - 1);
   }
   const int j = jn;
   const uint16_t* arow = p.a_store + un.aoff + int64_t(j < un.rows ? j : un.rows - 1) * p.k + un.kb + 8 * kg;
 #pragma unroll
-  for (int i = 0; i < kBatch; ++i) {
+  for (int i = 0; i < NB; ++i) {
     const int st = st0 + i * kProd;
     const int sc = st < un.steps ? st : max(un.steps - 1, 0);
     f.av[i] = global_load128_untracked(arow + 32 * sc);
@@ -408,19 +410,21 @@ __device__ __forceinline__ void first_frags(const GemvParams& p, const Unit& un,
 
 // Ties every fragment register to a wait already made (no use may be
 // scheduled above it).
-__device__ __forceinline__ void tie_frags(FirstFrags& f) {
+template <int NB>
+__device__ __forceinline__ void tie_frags(FirstFragsN<NB>& f) {
   tie(f.xc);
 #pragma unroll
-  for (int i = 0; i < kBatch; ++i) tie(f.av[i]);
+  for (int i = 0; i < NB; ++i) tie(f.av[i]);
 }
 
 // MFMAs of the first batch: step i's x fragment for lane (row jn, k-group
 // kg) comes from lane 4 i + kg of xc (row 0 only; other rows zero).
-__device__ __forceinline__ f32x4 first_mfma(const FirstFrags& f, const Unit& un, int st0, int lane, f32x4 c) {
+template <int NB>
+__device__ __forceinline__ f32x4 first_mfma(const FirstFragsN<NB>& f, const Unit& un, int st0, int lane, f32x4 c) {
   const int kg = lane >> 4;
   const bool row0 = (lane & 15) == 0;
 #pragma unroll
-  for (int i = 0; i < kBatch; ++i) {
+  for (int i = 0; i < NB; ++i) {
     const int src = (4 * i + kg) << 2;
     u32x4 x;
     x.x = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(f.xc.x)));
@@ -447,7 +451,8 @@ __device__ __forceinline__ f32x4 unit_mfma(const UnitFragsN<NB>& f, const Unit& 
 // higher j are never read). pre holds the first batch of row group 0 (already
 // landed); anything beyond it is loaded here. Then the wave counts itself
 // in (LDS) so the LoRA wave can publish without a workgroup barrier.
-__device__ void first_unit_partials(const GemvParams& p, const Unit& un, FirstFrags& pre, float* red, int* done,
+template <int NB>
+__device__ void first_unit_partials(const GemvParams& p, const Unit& un, FirstFragsN<NB>& pre, float* red, int* done,
                                     int wave, int lane) {
   tie_frags(pre);
   const int jn = lane & 15;
@@ -457,7 +462,7 @@ __device__ void first_unit_partials(const GemvParams& p, const Unit& un, FirstFr
     int st0 = wave;
     if (j0 == 0) {
       c = first_mfma(pre, un, st0, lane, c);
-      st0 += kBatch * kProd;
+      st0 += NB * kProd;
     }
     // Anything beyond the first batch (ranks above 16, long slices) in small
     // batches: this runs inside the base loop, where registers are scarce.
@@ -499,6 +504,7 @@ __device__ void publish_first_unit(const GemvParams& p, const float* red, const 
 // The LoRA wave alone: the workgroup's other units (only when there are
 // more units than producers, i.e. small grids), each contracted whole by
 // this wave and stored with the call's tag.
+template <int NB>
 __device__ void produce_other_units(const GemvParams& p, uint32_t tag, int lane) {
   if (blockIdx.x >= unsigned(p.producers)) return;
   const int jn = lane & 15;
@@ -508,9 +514,9 @@ __device__ void produce_other_units(const GemvParams& p, uint32_t tag, int lane)
     if (!unit_of(p, u, un)) continue;
     for (int j0 = 0; j0 < un.rows; j0 += 16) {
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
-      for (int st0 = 0; st0 < un.steps; st0 += kBatch) {
-        UnitFrags f;
-        unit_frags<false, kBatch>(p, un, j0, st0, 1, lane, f);
+      for (int st0 = 0; st0 < un.steps; st0 += NB) {
+        UnitFragsN<NB> f;
+        unit_frags<false, NB>(p, un, j0, st0, 1, lane, f);
         c = unit_mfma(f, un, st0, 1, c);
       }
       if (kg == 0 && j0 + jn < un.rows && !p.withhold) tagged_store(p.zp + partial_index(p, un, j0 + jn), c[0], tag);
@@ -713,7 +719,11 @@ __device__ __forceinline__ float full_dot(const GemvParams& p, int t, int g, int
 template <class TL, int KZ>
 __device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, uint32_t tag, int lane) {
   using L = LoraLds<TL>;
-  constexpr int kOut = 16 / KZ;  // values per lane and batch
+  // Values per lane and batch (16 entries; 8 for the smallest tile, whose
+  // one or two tokens need at most 2 x 16 x 16 partials at a 16-value z, and
+  // which keeps two workgroups per CU).
+  constexpr int kEntries = TL::kRT == 1 && TL::kXR == 2 ? 8 : 16;
+  constexpr int kOut = kEntries / KZ > 0 ? kEntries / KZ : 1;
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + L::kMeta);
   uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
   for (int e = lane; e < TL::kXR * 192 / 8; e += 64) reinterpret_cast<uint4*>(zl)[e] = make_uint4(0, 0, 0, 0);
@@ -984,8 +994,15 @@ __device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int
 // value in y, which the call updates in place with the LoRA delta
 // (y = bf16(bf16(y) + bf16(scale * z B^T)), the row_shrink + row_expand chain
 // in one launch); no weight stream, no bias.
+// Tile<1, 2> fits two workgroups per CU in LDS; its launch bounds ask for
+// the registers of two (four waves per SIMD), so one workgroup's prologue
+// and epilogue overlap the other's weight stream when N spans several rounds
+// of workgroups.
+template <int RT, int XR>
+constexpr int kMinWavesPerSimd = (RT == 1 && XR == 2) ? 4 : 2;
+
 template <int RT, int XR, bool kExact, bool kLora, bool kResidual = false>
-__global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv_kernel(GemvParams p) {
   using TL = Tile<RT, XR>;
   constexpr int TT = TL::kTT;
   constexpr int D = TL::kDepth;
@@ -1035,7 +1052,11 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
   // the unit's partials before their first stage.
   Unit un0{};
   bool has0 = false;
-  FirstFrags pre;
+  // Fragments of the first unit's first batch: ten steps per wave, four for
+  // the smallest tile (B <= 2, whose units span at most 28 steps at K up to
+  // 14336), which keeps that tile at two workgroups per CU.
+  constexpr int kFirst = (RT == 1 && XR == 2) ? 4 : kBatch;
+  FirstFragsN<kFirst> pre;
   TokenMeta tmeta{};
   uint32_t epoch = 0;
   int g_tile = -1, g_unit = -1;  // the LoRA wave: token slots loaded in the prologue
@@ -1114,7 +1135,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemv_kernel(GemvParams p) {
       const uint32_t tag = __builtin_amdgcn_readfirstlane(epoch) + 1u;
       lora_meta<TL>(lora_lds, tmeta, p.slices, lane);
       if (has0) publish_first_unit(p, red, &prod_done, un0, tag, lane);
-      produce_other_units(p, tag, lane);
+      produce_other_units<kFirst>(p, tag, lane);
     }
   }
 
