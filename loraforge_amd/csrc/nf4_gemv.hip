@@ -45,7 +45,7 @@ struct Tile {
   static constexpr int kScBytes = 256;  // one dword copy: kR * kSB scales used
   static constexpr int kStage = kWBytes + kXBytes + kScBytes;
   static constexpr int kDma = 2 + kXDma;  // copies per stage
-  static constexpr int kDepth = 3;
+  static constexpr int kDepth = (RT == 1 && XR == 8) ? 2 : 3;  // Tile<1, 8>: two workgroups per CU in LDS
   static_assert(kR * kSB * 32 <= kWBytes && kR * kSB <= 64, "stage sizes");
   static_assert(kDma * (kDepth - 1) < 64, "vmcnt range");
 };
@@ -719,10 +719,9 @@ __device__ __forceinline__ float full_dot(const GemvParams& p, int t, int g, int
 template <class TL, int KZ>
 __device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, uint32_t tag, int lane) {
   using L = LoraLds<TL>;
-  // Values per lane and batch (16 entries; 8 for the smallest tile, whose
-  // one or two tokens need at most 2 x 16 x 16 partials at a 16-value z, and
-  // which keeps two workgroups per CU).
-  constexpr int kEntries = TL::kRT == 1 && TL::kXR == 2 ? 8 : 16;
+  // Values per lane and batch (16 entries; 8 for the tiles of up to 8
+  // tokens, which keeps them at two workgroups per CU).
+  constexpr int kEntries = TL::kRT == 1 && TL::kXR <= 8 ? 8 : 16;
   constexpr int kOut = kEntries / KZ > 0 ? kEntries / KZ : 1;
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + L::kMeta);
   uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
@@ -999,7 +998,7 @@ __device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int
 // and epilogue overlap the other's weight stream when N spans several rounds
 // of workgroups.
 template <int RT, int XR>
-constexpr int kMinWavesPerSimd = (RT == 1 && XR == 2) ? 4 : 2;
+constexpr int kMinWavesPerSimd = (RT == 1 && XR <= 8) ? 4 : 2;
 
 template <int RT, int XR, bool kExact, bool kLora, bool kResidual = false>
 __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv_kernel(GemvParams p) {
@@ -1055,7 +1054,7 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   // Fragments of the first unit's first batch: ten steps per wave, four for
   // the smallest tile (B <= 2, whose units span at most 28 steps at K up to
   // 14336), which keeps that tile at two workgroups per CU.
-  constexpr int kFirst = (RT == 1 && XR == 2) ? 4 : kBatch;
+  constexpr int kFirst = (RT == 1 && XR <= 8) ? 4 : kBatch;
   FirstFragsN<kFirst> pre;
   TokenMeta tmeta{};
   uint32_t epoch = 0;
