@@ -1058,7 +1058,7 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   FirstFragsN<kFirst> pre;
   TokenMeta tmeta{};
   uint32_t epoch = 0;
-  int g_tile = -1, g_unit = -1;  // the LoRA wave: token slots loaded in the prologue
+  int g_tile = -1;  // the LoRA wave: token slots loaded in the prologue
   if (wave < kBase) {
     auto stage_kb = [&](int s) { return min(kb0 + s * TL::kSB, nblk - 1); };
     if constexpr (kLora) {
@@ -1087,8 +1087,6 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
     // dependent loads follow the barriers.
     epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     g_tile = p.token_slots[t0 + min(lane, mt - 1)];
-    const bool producer = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units;
-    g_unit = producer ? p.token_slots[unit_token(p, int(blockIdx.x))] : -1;
   }
   // Residual form: the summing waves (one per 16 x 16 tile) fetch the outputs
   // they will update now; nothing uses them before the end.
@@ -1125,15 +1123,17 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   __builtin_amdgcn_s_waitcnt(0xC07F);
   barrier_only();
   const uint32_t* ptl = pt + (lane % kCopies);
-  // The LoRA wave: tile metadata, then the first unit (published as soon as
-  // the contraction waves have counted in), the other units, then z.
+  // The LoRA wave: the first unit (found through scalar loads and published
+  // as soon as the contraction waves have counted in), then the tile
+  // metadata (its loads are requested first and land meanwhile), the other
+  // units, then z.
   if constexpr (kLora) {
     if (wave == kBase) {
       tmeta = token_meta(p, g_tile, mt, lane);
-      has0 = g_unit >= 0 && unit_of_slot(p, blockIdx.x, __builtin_amdgcn_readfirstlane(g_unit), un0);
+      has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
       const uint32_t tag = __builtin_amdgcn_readfirstlane(epoch) + 1u;
-      lora_meta<TL>(lora_lds, tmeta, p.slices, lane);
       if (has0) publish_first_unit(p, red, &prod_done, un0, tag, lane);
+      lora_meta<TL>(lora_lds, tmeta, p.slices, lane);
       produce_other_units<kFirst>(p, tag, lane);
     }
   }
