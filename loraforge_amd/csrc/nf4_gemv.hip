@@ -1068,13 +1068,20 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
     if constexpr (kLora && !kResidual) {
       // Workgroups that produce no unit hold their weight stream back by
       // about a microsecond (32 x 64 cycles), so the producers' unit
-      // fragments are ahead of it in the memory queues (measured against no
-      // delay: B = 1 13.4 -> 12.8 us, B = 8 14.8 -> 14.4 us, B = 64 19.0 ->
-      // 18.7 us; 12 x 64 cycles was worse, 48 x 64 no better). Producers
-      // hold their own stages back by half that, behind their fragments
-      // (B = 64 another -0.2 us).
-      if (!has0) __builtin_amdgcn_s_sleep(32);
-      else __builtin_amdgcn_s_sleep(16);
+      // fragments are ahead of it in the memory queues; producers hold
+      // their own stages back by half that, behind their fragments. The
+      // tiles of up to 8 tokens, whose LoRA chain is the longer path, hold
+      // back 48 x 64 cycles (24 for producers). Measured with the first unit
+      // published before the tile metadata: no delay c1 12.4 us, 16 x 64
+      // 11.1, 32 x 64 10.8, 48 x 64 10.5, 64 x 64 10.8, 96 x 64 11.7; B = 64
+      // 18.2 / 17.9 / 18.1 / 18.4 / 19.0 for no delay / 32 / 48 / 64 / 96.
+      if (kMinWavesPerSimd<RT, XR> > 2) {
+        if (!has0) __builtin_amdgcn_s_sleep(48);
+        else __builtin_amdgcn_s_sleep(24);
+      } else {
+        if (!has0) __builtin_amdgcn_s_sleep(32);
+        else __builtin_amdgcn_s_sleep(16);
+      }
     }
     if constexpr (!kResidual) {
 #pragma unroll
