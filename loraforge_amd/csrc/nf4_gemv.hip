@@ -595,14 +595,12 @@ __device__ __forceinline__ uint4 b8_fix(const uint4& v, const B8& b) {
 }
 
 // LDS of the LoRA stages, an array that never receives direct copies (so
-// stores into it do not wait for copies in flight): the tile metadata, z and
-// the partial staging area.
+// stores into it do not wait for copies in flight): the tile metadata and z.
 template <class TL>
 struct LoraLds {
   static constexpr int kMeta = 0;
-  static constexpr int kZ = 2048;                        // z: [tile token][3 slices][64] bf16
-  static constexpr int kStage = kZ + TL::kXR * 192 * 2;  // 4 KiB of partials
-  static constexpr int kBytes = kStage + 4096;
+  static constexpr int kZ = 2048;  // z: [tile token][3 slices][64] bf16
+  static constexpr int kBytes = kZ + TL::kXR * 192 * 2;
   static_assert(sizeof(TileMeta) <= 2048, "tile metadata");
 };
 
