@@ -816,17 +816,21 @@ __device__ void lora_gather(const GemvParams& p, char* lds, int t0, int mt, uint
 // over ranks in steps of 32, with z rows of other slots' tokens masked to
 // zero, into tiles of the base layout (token rows x 16 columns). Columns of
 // other slices are masked on the B side. B fragments go kSlotBatch slots
-// at a time, so one batch covers the at most 32 distinct slots of a tile;
-// it is requested as soon as the wave has finished its contraction and is
+// at a time, so one batch covers the distinct slots of a tile; it is
+// requested as soon as the wave has finished its contraction and is
 // shifted and masked (expand_b_fix) before the wait for z, so both its
 // latency and that VALU work overlap the wait.
 constexpr int kExpandWaves = kWaves - 1;
-constexpr int kSlotBatch = 5;
-static_assert(kSlotBatch * kExpandWaves >= 32, "one batch covers a tile's distinct slots");
+// Slots per wave and batch: enough for one batch to cover the at most
+// min(tile tokens, 32) distinct slots of a tile, and no more (every slot of a
+// batch is unrolled code that each workgroup runs once, after its weight
+// stream; c1 10.6 -> 10.2 us with one slot per wave instead of five).
+template <class TL>
+constexpr int kSlotBatch = (TL::kXR + kExpandWaves - 1) / kExpandWaves;
 
 template <class TL>
 struct ExpandB {
-  uint4 bf[kSlotBatch][TL::kRT];  // ranks 0..31 (ranks 32..63 are loaded where used)
+  uint4 bf[kSlotBatch<TL>][TL::kRT];  // ranks 0..31 (ranks 32..63 are loaded where used)
 };
 
 template <class TL>
@@ -836,7 +840,7 @@ __device__ __forceinline__ void expand_b_batch(const GemvParams& p, const TileMe
   const int kg = lane >> 4;
   const int nd = tm->nd;
 #pragma unroll
-  for (int q = 0; q < kSlotBatch; ++q) {
+  for (int q = 0; q < kSlotBatch<TL>; ++q) {
     const int d = d0 + q * kExpandWaves;
     const bool live = d < nd;
     const int dd = live ? d : 0;
@@ -859,7 +863,7 @@ __device__ __forceinline__ void expand_b_fix(const GemvParams& p, const TileMeta
   const int kg = lane >> 4;
   const int nd = tm->nd;
 #pragma unroll
-  for (int q = 0; q < kSlotBatch; ++q) {
+  for (int q = 0; q < kSlotBatch<TL>; ++q) {
     const int d = d0 + q * kExpandWaves;
     if (d >= nd) break;  // uniform
     const int st = tm->dstride[d];
@@ -910,13 +914,13 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
   const int top = hi + TL::kR / 2 - 1;
   const int s_lo = int(p.slices > 1 && lo >= bounds[1]) + int(p.slices > 2 && lo >= bounds[2]);
   const int s_hi = int(p.slices > 1 && top >= bounds[1]) + int(p.slices > 2 && top >= bounds[2]);
-  for (int d0 = wave; d0 < nd; d0 += kSlotBatch * kExpandWaves) {
+  for (int d0 = wave; d0 < nd; d0 += kSlotBatch<TL> * kExpandWaves) {
     if (d0 != wave) {
       expand_b_batch<TL>(p, tm, b, d0, lo, hi, lane);
       expand_b_fix<TL>(p, tm, b, d0, lo, hi, lane);
     }
 #pragma unroll
-    for (int q = 0; q < kSlotBatch; ++q) {
+    for (int q = 0; q < kSlotBatch<TL>; ++q) {
       const int d = d0 + q * kExpandWaves;
       if (d >= nd) break;  // uniform
       const int g = tm->dslot[d];
