@@ -42,7 +42,7 @@ constexpr int kMaxSlices = 4;
 constexpr int kShrinkWaves = 4;
 constexpr int kShrinkThreads = 64 * kShrinkWaves;
 constexpr int kShrinkBatch = 8;  // k steps per wave whose loads are in flight together
-constexpr int kMaxChunks = 16;   // K chunks of a split shrink
+constexpr int kMaxChunks = 4;    // K chunks of a split shrink (the summing code is unrolled over them)
 
 struct ShrinkArgs {
   const uint16_t* x;
@@ -425,7 +425,15 @@ struct ShrinkPlan {
 
 // Splits K across workgroups only for small token counts (decode), where one
 // workgroup per (slot, row tile) would leave most CUs idle and each of them
-// streaming a whole A tile; every chunk keeps at least one k step per wave.
+// streaming a whole A tile. Every chunk keeps at least kMinChunkSteps 32-wide
+// k steps: a finer split adds more to the partials' cross-workgroup round
+// trips than it takes off each workgroup's stream, and the summing
+// workgroup's gather is unrolled over kMaxChunks (c2, 64 tokens over 32
+// rank-16 adapters at K = 4096, shrink + expand: up to 16 chunks 19.5 us,
+// 8 chunks 16.9, 4 chunks with the gather unrolled over 16 slots 17.8 and
+// over 4 slots 16.2, 2 chunks 18.5, no split 20.2).
+constexpr int kMinChunkSteps = 32;
+
 ShrinkPlan plan_shrink(int64_t tokens, int64_t width, int64_t adapters, int slices, int max_rank) {
   ShrinkPlan pl{};
   const int64_t steps = (width + 31) / 32;
@@ -435,7 +443,7 @@ ShrinkPlan plan_shrink(int64_t tokens, int64_t width, int64_t adapters, int slic
   pl.group_cap = int(groups + (tokens + kShrinkThreads - 1) / kShrinkThreads);
   int64_t chunks = 1;
   if (tokens <= 256 && adapters * pl.row_tiles * pl.group_cap <= kMaxCounters)
-    while (active * pl.row_tiles * chunks * 2 <= kTargetGroups && steps >= chunks * 2 * kShrinkWaves &&
+    while (active * pl.row_tiles * chunks * 2 <= kTargetGroups && steps >= chunks * 2 * kMinChunkSteps &&
            chunks * 2 <= kMaxChunks)
       chunks *= 2;
   pl.chunk_steps = int((steps + chunks - 1) / chunks);
