@@ -32,23 +32,46 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kCopies = 16;  // pair-table copies (lane l reads copy l % 16)
 
 // RT: 16-row output tiles; XR: staged token rows (2, 8, 16 or 32).
+// kScPre (the tile of up to 2 tokens): each contraction wave copies the block
+// scales of its whole k range into LDS once, ahead of its first stage, and the
+// stages carry 4 blocks (a full 128-byte line of every row) two deep. The
+// other tiles copy each stage's scales with the stage. Measured read patterns
+// on MI355X (no arithmetic, 7 streaming waves, B = 1 x rows): 24576 x 4096
+// 18.9 -> 12.9 us, 4096 x 12288 11.6 -> 7.8 us, 4096 x 4096 5.0 -> 4.0 us.
 template <int RT, int XR>
 struct Tile {
   static constexpr int kRT = RT;
   static constexpr int kR = 16 * RT;
   static constexpr int kXR = XR;
   static constexpr int kTT = XR > 16 ? 2 : 1;                  // 16-token MFMA tiles
-  static constexpr int kSB = (RT == 1 && XR <= 16) ? 2 : 1;    // NF4 blocks per stage
-  static constexpr int kWBytes = 1024;                          // one copy: kR * kSB * 32 bytes used
+  static constexpr bool kScPre = RT == 1 && XR <= 2;
+  static constexpr int kSB = kScPre ? 4 : (RT == 1 && XR <= 16) ? 2 : 1;  // NF4 blocks per stage
+  static constexpr int kWBytes = kR * kSB * 32 < 1024 ? 1024 : kR * kSB * 32;
+  static constexpr int kWDma = kWBytes / 1024;
   static constexpr int kXBytes = XR * kSB * 128 < 1024 ? 1024 : XR * kSB * 128;
   static constexpr int kXDma = kXBytes / 1024;
-  static constexpr int kScBytes = 256;  // one dword copy: kR * kSB scales used
+  static constexpr int kScBytes = kScPre ? 0 : 256;  // one dword copy: kR * kSB scales used
   static constexpr int kStage = kWBytes + kXBytes + kScBytes;
-  static constexpr int kDma = 2 + kXDma;  // copies per stage
-  static constexpr int kDepth = (RT == 1 && XR == 8) ? 2 : 3;  // Tile<1, 8>: two workgroups per CU in LDS
-  static_assert(kR * kSB * 32 <= kWBytes && kR * kSB <= 64, "stage sizes");
+  static constexpr int kDma = kWDma + kXDma + (kScPre ? 0 : 1);  // copies per stage
+  // Tile<1, 8>: two workgroups per CU in LDS; Tile<1, 2>: 4-block stages.
+  static constexpr int kDepth = (RT == 1 && XR <= 8) ? 2 : 3;
+  static_assert(kR * kSB * 32 <= kWBytes && (kScPre || kR * kSB <= 64), "stage sizes");
   static_assert(kDma * (kDepth - 1) < 64, "vmcnt range");
 };
+
+// LDS scale area of one contraction wave (kScPre tiles): 16 rows of its k
+// range at a row stride of `stride` floats (odd: the 16 rows of a block fall
+// in distinct banks), rounded up to whole 64-lane dword copies.
+struct ScaleArea {
+  int stride;  // floats per row: (max blocks per wave) | 1
+  int bytes;   // per wave: multiple of 256
+};
+__host__ __device__ inline ScaleArea scale_area(int nblk, int waves) {
+  ScaleArea a;
+  a.stride = ((nblk + waves - 1) / waves) | 1;
+  a.bytes = (16 * a.stride * 4 + 255) / 256 * 256;
+  return a;
+}
 
 // bf16(silu(g)) * u in fp32 (the caller's store rounds the product): silu
 // as g / (1 + e^-g), the form of the reference's activation.
@@ -80,6 +103,8 @@ struct GemvParams {
   int64_t y_stride;
   int row_groups;  // n / R
   int gated_half;  // SwiGLU output: n / 2 (a group's rows: R / 2 gate rows and the matching up rows), else 0
+  int sc_stride;  // kScPre tiles: floats per row of a wave's scale area (odd)
+  int sc_bytes;   // kScPre tiles: bytes of a wave's scale area in dynamic LDS (multiple of 256)
   // LoRA (kLora variants only).
   const uint16_t* a_store;
   const int64_t* a_offsets;
@@ -100,6 +125,7 @@ struct GemvParams {
   uint32_t unit_inv;  // ceil(2^21 / (usplit * kz)): u / (usplit * kz) by a multiply (u <= 1024)
   int kz_len;     // k per slice (multiple of 64)
   int producers;  // workgroups b < producers make units b, b + producers, ...
+  int resident;   // workgroups of the first dispatch round (b < resident run beside the producers)
   int* status;    // set to 1 when a bounded wait for partials gave up (they were then recomputed)
   int spin_limit; // polls of a bounded wait for partials
   int withhold;   // test hook: producers publish nothing, so every wait gives up and recomputes
@@ -147,17 +173,19 @@ struct Frags {
   u32x4 xf[TL::kSB][TL::kTT][2];
 };
 
+// scb: the scales of the stage's first block (kScPre: in the wave's scale
+// area, rows srs bytes apart; else the stage's own scale slot).
 template <class TL>
-__device__ __forceinline__ void read_frags(Frags<TL>& f, uint32_t wbase, int n, int g) {
+__device__ __forceinline__ void read_frags(Frags<TL>& f, uint32_t wbase, uint32_t scb, uint32_t srs, int n, int g) {
   const uint32_t xbase = wbase + TL::kWBytes;
-  const uint32_t sbase = xbase + TL::kXBytes;
 #pragma unroll
   for (int b = 0; b < TL::kSB; ++b) {
 #pragma unroll
     for (int r = 0; r < TL::kRT; ++r) {
       const int row = r * 16 + n;
       f.q[b][r] = lds_read64(wbase + (b * TL::kR + row) * 32 + 8 * g);
-      f.sc[b][r] = lds_read32f(sbase + (b * TL::kR + row) * 4);
+      if constexpr (TL::kScPre) f.sc[b][r] = lds_read32f(scb + row * srs + b * 4);
+      else f.sc[b][r] = lds_read32f(scb + (b * TL::kR + row) * 4);
     }
 #pragma unroll
     for (int t = 0; t < TL::kTT; ++t) {
@@ -958,19 +986,21 @@ __device__ void expand_mfma(const GemvParams& p, const char* lds7, ExpandB<TL>& 
 // W: position p -> block p / (2R), row (p / 2) % R, 16-byte half p % 2, so a
 // block's rows are 32 contiguous bytes each. x: position p -> token row
 // p / (8 kSB), block (p / 8) % kSB, unit slot p % 8 holding 16-byte unit
-// (p % 8) ^ (row & 7) (conflict-free fragment reads). Scales: position
-// p -> block p / R, row p % R. Positions past the stage and blocks past the
-// wave's range read valid addresses of block kb (their scale is zeroed when
-// used). kb must be a valid block.
+// (p % 8) ^ (row & 7) (conflict-free fragment reads). Scales (tiles without
+// kScPre): position p -> block p / R, row p % R. Positions past the stage and
+// blocks past the wave's range read valid addresses of block kb (their scale
+// is zeroed when used). kb must be a valid block.
 template <class TL>
 __device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int lo, int hi, int t0, int mt, int kb,
                                             int kend, int lane) {
   const int nblk = p.k >> 6;
-  {
-    const int b = lane / (2 * TL::kR);
-    const int r = (lane >> 1) % TL::kR;
-    const int blk = (lane < 2 * TL::kR * TL::kSB && kb + b < kend) ? kb + b : kb;
-    copy16(p.q + int64_t(grow<TL>(lo, hi, r)) * (p.k >> 1) + blk * 32 + (lane & 1) * 16, slot);
+#pragma unroll
+  for (int d = 0; d < TL::kWDma; ++d) {
+    const int pos = d * 64 + lane;
+    const int b = pos / (2 * TL::kR);
+    const int r = (pos >> 1) % TL::kR;
+    const int blk = (pos < 2 * TL::kR * TL::kSB && kb + b < kend) ? kb + b : kb;
+    copy16(p.q + int64_t(grow<TL>(lo, hi, r)) * (p.k >> 1) + blk * 32 + (lane & 1) * 16, slot + d * 1024);
   }
 #pragma unroll
   for (int d = 0; d < TL::kXDma; ++d) {
@@ -983,11 +1013,29 @@ __device__ __forceinline__ void issue_stage(const GemvParams& p, char* slot, int
     const int tok = t0 + (row < mt ? row : mt - 1);
     copy16(p.x + int64_t(tok) * p.x_stride + blk * 64 + u * 8, slot + TL::kWBytes + d * 1024);
   }
-  {
+  if constexpr (!TL::kScPre) {
     const int b = lane / TL::kR;
     const int r = lane % TL::kR;
     const int blk = (lane < TL::kR * TL::kSB && kb + b < kend) ? kb + b : kb;
     copy4(p.scales + int64_t(grow<TL>(lo, hi, r)) * nblk + (blk < nblk ? blk : 0), slot + TL::kWBytes + TL::kXBytes);
+  }
+}
+
+// kScPre: the block scales of the group's 16 rows over the wave's blocks
+// kb0 .. kb0 + nbw - 1 into its scale area (row j at j * stride floats), as
+// dword copies of 64 consecutive floats. Padding positions read a valid scale
+// of the range (never used). kb0 must be a valid block.
+template <class TL>
+__device__ __forceinline__ void issue_scales(const GemvParams& p, char* area, int lo, int hi, int kb0, int nbw,
+                                             int lane) {
+  const int nblk = p.k >> 6;
+  for (int i = 0; i < p.sc_bytes / 256; ++i) {
+    const int pos = i * 64 + lane;
+    int row = pos / p.sc_stride;
+    int col = pos - row * p.sc_stride;
+    if (row > TL::kR - 1) row = TL::kR - 1;
+    if (col >= nbw) col = 0;
+    copy4(p.scales + int64_t(grow<TL>(lo, hi, row)) * nblk + kb0 + col, area + i * 256);
   }
 }
 
@@ -1016,6 +1064,7 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   __shared__ float red[kLora ? kProd * 192 : 1];
   __shared__ int prod_done;  // contraction waves that have written their first-unit partials
   __shared__ f32x4 up_vals[RT == 2 ? TL::kTT * 64 : 1];  // SwiGLU output: the up tile's final values
+  extern __shared__ __attribute__((aligned(16))) char scale_lds[];  // kScPre: kBase * p.sc_bytes (+16)
 
   const int rg = blockIdx.x % p.row_groups;
   const int tile = blockIdx.x / p.row_groups;
@@ -1032,6 +1081,7 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   const int kend = wave < kBase ? nblk * (wave + 1) / kBase : 0;
   const int nst = kResidual ? 0 : (kend - kb0 + TL::kSB - 1) / TL::kSB;
   char* myring = ring + wave * D * TL::kStage;  // waves below kBase only
+  char* myscales = scale_lds + wave * p.sc_bytes;  // kScPre, waves below kBase only
   static_assert(!kResidual || (kLora && !kExact), "the residual form is a LoRA-only variant");
 
   // Codebook (and the LoRA slice bounds) through scalar loads: no vector
@@ -1063,6 +1113,9 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   int g_tile = -1;  // the LoRA wave: token slots loaded in the prologue
   if (wave < kBase) {
     auto stage_kb = [&](int s) { return min(kb0 + s * TL::kSB, nblk - 1); };
+    // kScPre: the wave's scales first (the wait for its first stage covers
+    // them, and the unit's fragments are not queued behind them for long).
+    if constexpr (TL::kScPre && !kResidual) issue_scales<TL>(p, myscales, lo, hi, kb0, kend - kb0, lane);
     if constexpr (kLora) {
       has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
       if (has0) first_frags(p, un0, wave, lane, pre);
@@ -1077,12 +1130,16 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
       // published before the tile metadata: no delay c1 12.4 us, 16 x 64
       // 11.1, 32 x 64 10.8, 48 x 64 10.5, 64 x 64 10.8, 96 x 64 11.7; B = 64
       // 18.2 / 17.9 / 18.1 / 18.4 / 19.0 for no delay / 32 / 48 / 64 / 96.
-      if (kMinWavesPerSimd<RT, XR> > 2) {
-        if (!has0) __builtin_amdgcn_s_sleep(48);
-        else __builtin_amdgcn_s_sleep(24);
-      } else {
-        if (!has0) __builtin_amdgcn_s_sleep(32);
-        else __builtin_amdgcn_s_sleep(16);
+      // Workgroups of later dispatch rounds start after the producers have
+      // published and do not wait.
+      if (int(blockIdx.x) < p.resident) {
+        if (kMinWavesPerSimd<RT, XR> > 2) {
+          if (!has0) __builtin_amdgcn_s_sleep(48);
+          else __builtin_amdgcn_s_sleep(24);
+        } else {
+          if (!has0) __builtin_amdgcn_s_sleep(32);
+          else __builtin_amdgcn_s_sleep(16);
+        }
       }
     }
     if constexpr (!kResidual) {
@@ -1170,28 +1227,54 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
       first_unit_partials(p, un0, pre, red, &prod_done, wave, lane);
     }
   }
-  if (nst > 0) {
-    wait_stages<TL>(min(D - 1, nst - 1));
-    read_frags<TL>(cur, ring_base, n, g);
-    settle(cur);
-  }
-  // One ring stage: read the next stage's fragments, refill, contract this
-  // one.
-  auto step = [&](int s) {
-    const bool more = s + 1 < nst;
-    if (more) {
-      wait_stages<TL>(min(D - 2, nst - 2 - s));
-      read_frags<TL>(nxt, ring_base + ((s + 1) % D) * TL::kStage, n, g);
-    }
-    if (s + D < nst)
-      issue_stage<TL>(p, myring + (s % D) * TL::kStage, lo, hi, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
-    contract<TL, kExact>(cur, kb0 + s * TL::kSB, kend, acc, table, ptl);
-    if (more) {
-      settle(nxt);
-      cur = nxt;
-    }
+  // Scales of stage s: kScPre tiles read the wave's scale area (block
+  // kb0 + s kSB onwards), the others the stage's slot.
+  const uint32_t sc_base = lds_addr(myscales);
+  const uint32_t sc_rs = uint32_t(p.sc_stride) * 4;
+  auto scb_of = [&](int s) -> uint32_t {
+    if constexpr (TL::kScPre) return sc_base + uint32_t(s * TL::kSB) * 4;
+    else return ring_base + (s % D) * TL::kStage + TL::kWBytes + TL::kXBytes;
   };
-  for (int s = 0; s < nst; ++s) step(s);
+  // kAhead: stage s + 1's fragments are read while stage s is contracted
+  // (D - 1 stages stream meanwhile); otherwise each stage's fragments are read
+  // at the top of its step and its slot refilled at once (D stages stream).
+  // The 4-block stages of the kScPre tile do not fit two fragment sets in
+  // registers, and streaming two of them per wave is what their two-deep
+  // ring is for (c3 down projection at B = 1: 17.2 -> 14.6 us).
+  constexpr bool kAhead = !TL::kScPre;
+  if constexpr (kAhead) {
+    if (nst > 0) {
+      wait_stages<TL>(min(D - 1, nst - 1));
+      read_frags<TL>(cur, ring_base, scb_of(0), sc_rs, n, g);
+      settle(cur);
+    }
+    // One ring stage: read the next stage's fragments, refill, contract this
+    // one.
+    auto step = [&](int s) {
+      const bool more = s + 1 < nst;
+      if (more) {
+        wait_stages<TL>(min(D - 2, nst - 2 - s));
+        read_frags<TL>(nxt, ring_base + ((s + 1) % D) * TL::kStage, scb_of(s + 1), sc_rs, n, g);
+      }
+      if (s + D < nst)
+        issue_stage<TL>(p, myring + (s % D) * TL::kStage, lo, hi, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
+      contract<TL, kExact>(cur, kb0 + s * TL::kSB, kend, acc, table, ptl);
+      if (more) {
+        settle(nxt);
+        cur = nxt;
+      }
+    };
+    for (int s = 0; s < nst; ++s) step(s);
+  } else {
+    for (int s = 0; s < nst; ++s) {
+      wait_stages<TL>(min(D - 1, nst - 1 - s));
+      read_frags<TL>(cur, ring_base + (s % D) * TL::kStage, scb_of(s), sc_rs, n, g);
+      settle(cur);
+      if (s + D < nst)
+        issue_stage<TL>(p, myring + (s % D) * TL::kStage, lo, hi, t0, mt, kb0 + (s + D) * TL::kSB, kend, lane);
+      contract<TL, kExact>(cur, kb0 + s * TL::kSB, kend, acc, table, ptl);
+    }
+  }
 
   // Sum the waves' partial tiles: wave w writes its tiles into its own ring
   // (all of its copies have landed), then tile c = wave is summed by wave c.
@@ -1302,17 +1385,18 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   if (kLora && wave == kBase) depart_finish(p.ce, departed, __builtin_amdgcn_readfirstlane(epoch), lane);
 }
 
+// lds: dynamic LDS bytes (the kScPre tiles' scale areas).
 template <int RT, int XR, bool kLora>
-void launch_exact(bool exact, dim3 grid, hipStream_t s, const GemvParams& p) {
-  if (exact) hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, true, kLora>), grid, dim3(kThreads), 0, s, p);
-  else hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, kLora>), grid, dim3(kThreads), 0, s, p);
+void launch_exact(bool exact, dim3 grid, size_t lds, hipStream_t s, const GemvParams& p) {
+  if (exact) hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, true, kLora>), grid, dim3(kThreads), lds, s, p);
+  else hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, kLora>), grid, dim3(kThreads), lds, s, p);
 }
 
 template <int RT, int XR>
-void launch_tile(bool exact, bool lora, bool residual, dim3 grid, hipStream_t s, const GemvParams& p) {
+void launch_tile(bool exact, bool lora, bool residual, dim3 grid, size_t lds, hipStream_t s, const GemvParams& p) {
   if (residual) hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, true, true>), grid, dim3(kThreads), 0, s, p);
-  else if (lora) launch_exact<RT, XR, true>(exact, grid, s, p);
-  else launch_exact<RT, XR, false>(exact, grid, s, p);
+  else if (lora) launch_exact<RT, XR, true>(exact, grid, lds, s, p);
+  else launch_exact<RT, XR, false>(exact, grid, lds, s, p);
 }
 
 struct GemvPlan {
@@ -1433,6 +1517,8 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
     LF_REQUIRE(pl.units <= 1024, "too many shrink units");
     p.kz_len = pl.kz_len;
     p.producers = pl.producers;
+    // Tiles of at most 8 tokens run two workgroups per CU.
+    p.resident = std::min(pl.grid, device_cus() * (m <= 8 ? 2 : 1));
     char* ws = static_cast<char*>(workspace);
     p.ce = call_epoch_of(ws);
     p.status = reinterpret_cast<int*>(ws + kStatusOffset);
@@ -1443,11 +1529,21 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   const dim3 grid(unsigned(pl.grid));
   auto s = static_cast<hipStream_t>(stream);
   const bool lo = lora != nullptr;
-  if (m <= 2) launch_tile<1, 2>(exact, lo, residual, grid, s, p);
-  else if (m <= 8) launch_tile<1, 8>(exact, lo, residual, grid, s, p);
-  else if (m <= 16) launch_tile<1, 16>(exact, lo, residual, grid, s, p);
-  else if (m <= 32) launch_tile<1, 32>(exact, lo, residual, grid, s, p);
-  else launch_tile<2, 32>(exact, lo, residual, grid, s, p);
+  // The tile of up to 2 tokens (kScPre) keeps each contraction wave's block
+  // scales in dynamic LDS (16 trailing bytes: the last area's stage reads may
+  // run up to 3 floats past it).
+  size_t lds = 0;
+  if (m <= 2 && !residual) {
+    const ScaleArea a = scale_area(int(w->k / 64), lo ? kWaves - 1 : kWaves);
+    p.sc_stride = a.stride;
+    p.sc_bytes = a.bytes;
+    lds = size_t(lo ? kWaves - 1 : kWaves) * size_t(a.bytes) + 16;
+  }
+  if (m <= 2) launch_tile<1, 2>(exact, lo, residual, grid, lds, s, p);
+  else if (m <= 8) launch_tile<1, 8>(exact, lo, residual, grid, 0, s, p);
+  else if (m <= 16) launch_tile<1, 16>(exact, lo, residual, grid, 0, s, p);
+  else if (m <= 32) launch_tile<1, 32>(exact, lo, residual, grid, 0, s, p);
+  else launch_tile<2, 32>(exact, lo, residual, grid, 0, s, p);
   LF_HIP(hipGetLastError());
   return kOk;
 }
