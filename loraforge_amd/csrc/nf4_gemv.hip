@@ -32,20 +32,22 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kCopies = 16;  // pair-table copies (lane l reads copy l % 16)
 
 // RT: 16-row output tiles; XR: staged token rows (2, 8, 16 or 32).
-// kScPre (the tile of up to 2 tokens): each contraction wave copies the block
-// scales of its whole k range into LDS once, ahead of its first stage, and the
-// stages carry 4 blocks (a full 128-byte line of every row) two deep. The
-// other tiles copy each stage's scales with the stage. Measured read patterns
-// on MI355X (no arithmetic, 7 streaming waves, B = 1 x rows): 24576 x 4096
-// 18.9 -> 12.9 us, 4096 x 12288 11.6 -> 7.8 us, 4096 x 4096 5.0 -> 4.0 us.
+// kScPre (the tiles of up to 8 tokens): each contraction wave copies the block
+// scales of its whole k range into LDS once, ahead of its first stage; the
+// tile of up to 2 tokens also stages 4 blocks (a full 128-byte line of every
+// row) at a time. The other tiles copy each stage's scales with the stage.
+// Measured read patterns on MI355X (no arithmetic, 7 streaming waves, B = 1
+// x rows, per-stage scales and 2-block stages -> scales once and 4-block
+// stages): 24576 x 4096 18.9 -> 12.9 us, 4096 x 12288 11.6 -> 7.8 us,
+// 4096 x 4096 5.0 -> 4.0 us.
 template <int RT, int XR>
 struct Tile {
   static constexpr int kRT = RT;
   static constexpr int kR = 16 * RT;
   static constexpr int kXR = XR;
   static constexpr int kTT = XR > 16 ? 2 : 1;                  // 16-token MFMA tiles
-  static constexpr bool kScPre = RT == 1 && XR <= 2;
-  static constexpr int kSB = kScPre ? 4 : (RT == 1 && XR <= 16) ? 2 : 1;  // NF4 blocks per stage
+  static constexpr bool kScPre = RT == 1 && XR <= 8;
+  static constexpr int kSB = XR <= 2 ? 4 : (RT == 1 && XR <= 16) ? 2 : 1;  // NF4 blocks per stage
   static constexpr int kWBytes = kR * kSB * 32 < 1024 ? 1024 : kR * kSB * 32;
   static constexpr int kWDma = kWBytes / 1024;
   static constexpr int kXBytes = XR * kSB * 128 < 1024 ? 1024 : XR * kSB * 128;
@@ -1238,9 +1240,10 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   // kAhead: stage s + 1's fragments are read while stage s is contracted
   // (D - 1 stages stream meanwhile); otherwise each stage's fragments are read
   // at the top of its step and its slot refilled at once (D stages stream).
-  // The 4-block stages of the kScPre tile do not fit two fragment sets in
-  // registers, and streaming two of them per wave is what their two-deep
-  // ring is for (c3 down projection at B = 1: 17.2 -> 14.6 us).
+  // The kScPre tiles run two-deep rings, both slots streaming (their 4-block
+  // stages would not fit two fragment sets in registers either): c3 down
+  // projection 17.2 -> 14.6 us at B = 1, 20.2 -> 17.9 us at B = 8 (with the
+  // scales in LDS).
   constexpr bool kAhead = !TL::kScPre;
   if constexpr (kAhead) {
     if (nst > 0) {
@@ -1529,18 +1532,18 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   const dim3 grid(unsigned(pl.grid));
   auto s = static_cast<hipStream_t>(stream);
   const bool lo = lora != nullptr;
-  // The tile of up to 2 tokens (kScPre) keeps each contraction wave's block
+  // The tiles of up to 8 tokens (kScPre) keep each contraction wave's block
   // scales in dynamic LDS (16 trailing bytes: the last area's stage reads may
   // run up to 3 floats past it).
   size_t lds = 0;
-  if (m <= 2 && !residual) {
+  if (m <= 8 && !residual) {
     const ScaleArea a = scale_area(int(w->k / 64), lo ? kWaves - 1 : kWaves);
     p.sc_stride = a.stride;
     p.sc_bytes = a.bytes;
     lds = size_t(lo ? kWaves - 1 : kWaves) * size_t(a.bytes) + 16;
   }
   if (m <= 2) launch_tile<1, 2>(exact, lo, residual, grid, lds, s, p);
-  else if (m <= 8) launch_tile<1, 8>(exact, lo, residual, grid, 0, s, p);
+  else if (m <= 8) launch_tile<1, 8>(exact, lo, residual, grid, lds, s, p);
   else if (m <= 16) launch_tile<1, 16>(exact, lo, residual, grid, 0, s, p);
   else if (m <= 32) launch_tile<1, 32>(exact, lo, residual, grid, 0, s, p);
   else launch_tile<2, 32>(exact, lo, residual, grid, 0, s, p);
