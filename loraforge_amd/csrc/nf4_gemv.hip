@@ -32,22 +32,22 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kCopies = 16;  // pair-table copies (lane l reads copy l % 16)
 
 // RT: 16-row output tiles; XR: staged token rows (2, 8, 16 or 32).
-// kScPre (the tiles of up to 8 tokens): each contraction wave copies the block
-// scales of its whole k range into LDS once, ahead of its first stage; the
-// tile of up to 2 tokens also stages 4 blocks (a full 128-byte line of every
-// row) at a time. The other tiles copy each stage's scales with the stage.
-// Measured read patterns on MI355X (no arithmetic, 7 streaming waves, B = 1
-// x rows, per-stage scales and 2-block stages -> scales once and 4-block
-// stages): 24576 x 4096 18.9 -> 12.9 us, 4096 x 12288 11.6 -> 7.8 us,
-// 4096 x 4096 5.0 -> 4.0 us.
-template <int RT, int XR>
+// SP (scales in LDS; the launch uses it wherever the scale areas fit): each
+// contraction wave copies the block scales of its whole k range into LDS
+// once, ahead of its first stage, and the tile of up to 2 tokens stages 4
+// blocks (a full 128-byte line of every row) at a time. Otherwise each stage
+// carries its own scales. Measured read patterns on MI355X (no arithmetic,
+// 7 streaming waves, B = 1 x rows, per-stage scales and 2-block stages ->
+// scales once and 4-block stages): 24576 x 4096 18.9 -> 12.9 us, 4096 x 12288
+// 11.6 -> 7.8 us, 4096 x 4096 5.0 -> 4.0 us.
+template <int RT, int XR, bool SP>
 struct Tile {
   static constexpr int kRT = RT;
   static constexpr int kR = 16 * RT;
   static constexpr int kXR = XR;
   static constexpr int kTT = XR > 16 ? 2 : 1;                  // 16-token MFMA tiles
-  static constexpr bool kScPre = RT == 1 && XR <= 8;
-  static constexpr int kSB = XR <= 2 ? 4 : (RT == 1 && XR <= 16) ? 2 : 1;  // NF4 blocks per stage
+  static constexpr bool kScPre = SP;
+  static constexpr int kSB = (SP && XR <= 2) ? 4 : (RT == 1 && XR <= 16) ? 2 : 1;  // NF4 blocks per stage
   static constexpr int kWBytes = kR * kSB * 32 < 1024 ? 1024 : kR * kSB * 32;
   static constexpr int kWDma = kWBytes / 1024;
   static constexpr int kXBytes = XR * kSB * 128 < 1024 ? 1024 : XR * kSB * 128;
@@ -56,22 +56,23 @@ struct Tile {
   static constexpr int kStage = kWBytes + kXBytes + kScBytes;
   static constexpr int kDma = kWDma + kXDma + (kScPre ? 0 : 1);  // copies per stage
   // Tile<1, 8>: two workgroups per CU in LDS; Tile<1, 2>: 4-block stages.
-  static constexpr int kDepth = (RT == 1 && XR <= 8) ? 2 : 3;
+  static constexpr int kDepth = (RT == 1 && (XR == 8 || (SP && XR <= 2))) ? 2 : 3;
   static_assert(kR * kSB * 32 <= kWBytes && (kScPre || kR * kSB <= 64), "stage sizes");
   static_assert(kDma * (kDepth - 1) < 64, "vmcnt range");
 };
 
-// LDS scale area of one contraction wave (kScPre tiles): 16 rows of its k
-// range at a row stride of `stride` floats (odd: the 16 rows of a block fall
-// in distinct banks), rounded up to whole 64-lane dword copies.
+// LDS scale area of one contraction wave (kScPre tiles): the group's rows
+// over its k range at a row stride of `stride` floats (odd: the 16 rows a
+// fragment read covers fall in distinct banks), rounded up to whole 64-lane
+// dword copies.
 struct ScaleArea {
   int stride;  // floats per row: (max blocks per wave) | 1
   int bytes;   // per wave: multiple of 256
 };
-__host__ __device__ inline ScaleArea scale_area(int nblk, int waves) {
+inline ScaleArea scale_area(int nblk, int waves, int rows) {
   ScaleArea a;
   a.stride = ((nblk + waves - 1) / waves) | 1;
-  a.bytes = (16 * a.stride * 4 + 255) / 256 * 256;
+  a.bytes = int((int64_t(rows) * a.stride * 4 + 255) / 256 * 256);
   return a;
 }
 
@@ -1052,9 +1053,9 @@ __device__ __forceinline__ void issue_scales(const GemvParams& p, char* area, in
 template <int RT, int XR>
 constexpr int kMinWavesPerSimd = (RT == 1 && XR <= 8) ? 4 : 2;
 
-template <int RT, int XR, bool kExact, bool kLora, bool kResidual = false>
+template <int RT, int XR, bool kExact, bool kLora, bool kResidual, bool kSP>
 __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv_kernel(GemvParams p) {
-  using TL = Tile<RT, XR>;
+  using TL = Tile<RT, XR, kSP>;
   constexpr int TT = TL::kTT;
   constexpr int D = TL::kDepth;
   constexpr int kBase = kLora ? kWaves - 1 : kWaves;  // waves on the base contraction (ring owners)
@@ -1240,10 +1241,10 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   // kAhead: stage s + 1's fragments are read while stage s is contracted
   // (D - 1 stages stream meanwhile); otherwise each stage's fragments are read
   // at the top of its step and its slot refilled at once (D stages stream).
-  // The kScPre tiles run two-deep rings, both slots streaming (their 4-block
-  // stages would not fit two fragment sets in registers either): c3 down
-  // projection 17.2 -> 14.6 us at B = 1, 20.2 -> 17.9 us at B = 8 (with the
-  // scales in LDS).
+  // With the scales in LDS every stage streams (the 4-block stages would not
+  // fit two fragment sets in registers either): c3 down projection
+  // 17.2 -> 14.6 us at B = 1, 20.2 -> 17.9 us at B = 8; north-star B = 64
+  // 18.4 -> 18.1 us (base only 11.8 -> 10.9 us).
   constexpr bool kAhead = !TL::kScPre;
   if constexpr (kAhead) {
     if (nst > 0) {
@@ -1388,18 +1389,42 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   if (kLora && wave == kBase) depart_finish(p.ce, departed, __builtin_amdgcn_readfirstlane(epoch), lane);
 }
 
-// lds: dynamic LDS bytes (the kScPre tiles' scale areas).
-template <int RT, int XR, bool kLora>
-void launch_exact(bool exact, dim3 grid, size_t lds, hipStream_t s, const GemvParams& p) {
-  if (exact) hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, true, kLora>), grid, dim3(kThreads), lds, s, p);
-  else hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, kLora>), grid, dim3(kThreads), lds, s, p);
+constexpr int64_t kLdsBytes = 160 * 1024;  // LDS of one workgroup on gfx950
+
+// Launches the variant with the block scales in LDS (each contraction wave's
+// area in dynamic LDS, 16 trailing bytes: the last area's stage reads may run
+// up to 3 floats past it) when its static LDS and the areas fit, else the
+// variant that stages the scales with the weights (very long K).
+template <int RT, int XR, bool kExact, bool kLora>
+int launch_scaled(dim3 grid, hipStream_t s, GemvParams p) {
+  constexpr int kBase = kLora ? kWaves - 1 : kWaves;
+  auto fn = nf4_gemv_kernel<RT, XR, kExact, kLora, false, true>;
+  static int64_t static_lds = -1;  // per kernel, queried once
+  if (static_lds < 0) {
+    hipFuncAttributes at{};
+    LF_HIP(hipFuncGetAttributes(&at, reinterpret_cast<const void*>(fn)));
+    static_lds = int64_t(at.sharedSizeBytes);
+  }
+  const ScaleArea a = scale_area(p.k >> 6, kBase, 16 * RT);
+  const int64_t dyn = int64_t(kBase) * a.bytes + 16;
+  if (static_lds + dyn <= kLdsBytes) {
+    p.sc_stride = a.stride;
+    p.sc_bytes = a.bytes;
+    hipLaunchKernelGGL(fn, grid, dim3(kThreads), size_t(dyn), s, p);
+  } else {
+    hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, kExact, kLora, false, false>), grid, dim3(kThreads), 0, s, p);
+  }
+  return kOk;
 }
 
 template <int RT, int XR>
-void launch_tile(bool exact, bool lora, bool residual, dim3 grid, size_t lds, hipStream_t s, const GemvParams& p) {
-  if (residual) hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, true, true>), grid, dim3(kThreads), 0, s, p);
-  else if (lora) launch_exact<RT, XR, true>(exact, grid, lds, s, p);
-  else launch_exact<RT, XR, false>(exact, grid, lds, s, p);
+int launch_tile(bool exact, bool lora, bool residual, dim3 grid, hipStream_t s, const GemvParams& p) {
+  if (residual) {
+    hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, true, true, false>), grid, dim3(kThreads), 0, s, p);
+    return kOk;
+  }
+  if (lora) return exact ? launch_scaled<RT, XR, true, true>(grid, s, p) : launch_scaled<RT, XR, false, true>(grid, s, p);
+  return exact ? launch_scaled<RT, XR, true, false>(grid, s, p) : launch_scaled<RT, XR, false, false>(grid, s, p);
 }
 
 struct GemvPlan {
@@ -1532,21 +1557,13 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   const dim3 grid(unsigned(pl.grid));
   auto s = static_cast<hipStream_t>(stream);
   const bool lo = lora != nullptr;
-  // The tiles of up to 8 tokens (kScPre) keep each contraction wave's block
-  // scales in dynamic LDS (16 trailing bytes: the last area's stage reads may
-  // run up to 3 floats past it).
-  size_t lds = 0;
-  if (m <= 8 && !residual) {
-    const ScaleArea a = scale_area(int(w->k / 64), lo ? kWaves - 1 : kWaves);
-    p.sc_stride = a.stride;
-    p.sc_bytes = a.bytes;
-    lds = size_t(lo ? kWaves - 1 : kWaves) * size_t(a.bytes) + 16;
-  }
-  if (m <= 2) launch_tile<1, 2>(exact, lo, residual, grid, lds, s, p);
-  else if (m <= 8) launch_tile<1, 8>(exact, lo, residual, grid, lds, s, p);
-  else if (m <= 16) launch_tile<1, 16>(exact, lo, residual, grid, 0, s, p);
-  else if (m <= 32) launch_tile<1, 32>(exact, lo, residual, grid, 0, s, p);
-  else launch_tile<2, 32>(exact, lo, residual, grid, 0, s, p);
+  int rc;
+  if (m <= 2) rc = launch_tile<1, 2>(exact, lo, residual, grid, s, p);
+  else if (m <= 8) rc = launch_tile<1, 8>(exact, lo, residual, grid, s, p);
+  else if (m <= 16) rc = launch_tile<1, 16>(exact, lo, residual, grid, s, p);
+  else if (m <= 32) rc = launch_tile<1, 32>(exact, lo, residual, grid, s, p);
+  else rc = launch_tile<2, 32>(exact, lo, residual, grid, s, p);
+  if (rc != kOk) return rc;
   LF_HIP(hipGetLastError());
   return kOk;
 }

@@ -3,7 +3,8 @@
 Every tile shape of the decode kernel (16 rows x 2 / 8 / 16 / 32 staged
 tokens, 32 rows x 32 tokens with two token tiles), token counts that leave
 ragged tiles, bias, a strided x, widths that are not a multiple of the row
-tile, long K (12288), repeated calls on one workspace and graph replays.
+tile, long K (12288, and 131072 where the block scales no longer fit LDS),
+repeated calls on one workspace and graph replays.
 Gate: max abs/rel 2e-2 and relative L2 < 0.005.
 """
 
@@ -44,6 +45,23 @@ def test_decode_base_odd_shapes(m, n, k, device):
     y = nf4_lora_linear(x, q, st)
     torch.cuda.synchronize()
     close(bits(y), _base_expected(case))
+
+
+@pytest.mark.parametrize("m,with_lora", [(2, False), (2, True), (8, True), (20, True), (64, True)])
+def test_decode_very_long_k(m, with_lora, device):
+    """K = 131072: a wave's block scales no longer fit in LDS beside its ring, so
+    the launch takes the variant that stages the scales with the weights (every
+    tile; the 32-row tile already does at K = 12288, covered above). W is drawn
+    8x narrower than elsewhere so the outputs stay O(1): the default arithmetic
+    (bf16 codes, fp32 block scale on the block sum) differs from the
+    dequantised-weight product by one bf16 rounding per weight, a difference
+    that grows as sqrt(K) (at W ~ N(0, 0.02) about 0.014 rms here)."""
+    case = _cases.fused_case(m, 64, 131072, ranks=(8, 16), seed=990 + m, null_frac=0.0, w_std=0.0025)
+    x, q, st, lora, _ = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, lora=lora if with_lora else None)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case) if with_lora else _base_expected(case))
+    assert decode_status(device=device) == 0
 
 
 @pytest.mark.parametrize("m", [1, 64])
