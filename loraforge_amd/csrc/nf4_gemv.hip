@@ -1128,17 +1128,17 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
       // about a microsecond (32 x 64 cycles), so the producers' unit
       // fragments are ahead of it in the memory queues; producers hold
       // their own stages back by half that, behind their fragments. The
-      // tiles of up to 8 tokens, whose LoRA chain is the longer path, hold
-      // back 48 x 64 cycles (24 for producers). Measured with the first unit
-      // published before the tile metadata: no delay c1 12.4 us, 16 x 64
-      // 11.1, 32 x 64 10.8, 48 x 64 10.5, 64 x 64 10.8, 96 x 64 11.7; B = 64
-      // 18.2 / 17.9 / 18.1 / 18.4 / 19.0 for no delay / 32 / 48 / 64 / 96.
+      // tiles of up to 8 tokens hold back 24 x 64 cycles (12 for producers):
+      // with the block scales in LDS, c1 9.78 / 9.80 / 9.86 / 9.99 us for
+      // 24 / 32 / 48 / 64 x 64 (B = 64: 18.2 / 17.9 / 18.1 / 18.4 / 19.0 us
+      // for no delay / 32 / 48 / 64 / 96 x 64, measured on an older stage
+      // layout).
       // Workgroups of later dispatch rounds start after the producers have
       // published and do not wait.
       if (int(blockIdx.x) < p.resident) {
         if (kMinWavesPerSimd<RT, XR> > 2) {
-          if (!has0) __builtin_amdgcn_s_sleep(48);
-          else __builtin_amdgcn_s_sleep(24);
+          if (!has0) __builtin_amdgcn_s_sleep(24);
+          else __builtin_amdgcn_s_sleep(12);
         } else {
           if (!has0) __builtin_amdgcn_s_sleep(32);
           else __builtin_amdgcn_s_sleep(16);
