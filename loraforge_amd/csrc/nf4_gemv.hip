@@ -32,8 +32,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kCopies = 16;  // pair-table copies (lane l reads copy l % 16)
 
 // RT: 16-row output tiles; XR: staged token rows (2, 8, 16 or 32).
-// SP: 0 per-stage scales, 1 scales in LDS, 2 scales in LDS with a two-deep
-// ring (the launch takes the first of 1, 2, 0 whose LDS fits). With SP > 0 each
+// SP (scales in LDS; the launch uses it wherever the scale areas fit): each
 // contraction wave copies the block scales of its whole k range into LDS
 // once, ahead of its first stage, and the tile of up to 2 tokens stages 4
 // blocks (a full 128-byte line of every row) at a time. Otherwise each stage
@@ -41,13 +40,13 @@ constexpr int kCopies = 16;  // pair-table copies (lane l reads copy l % 16)
 // 7 streaming waves, B = 1 x rows, per-stage scales and 2-block stages ->
 // scales once and 4-block stages): 24576 x 4096 18.9 -> 12.9 us, 4096 x 12288
 // 11.6 -> 7.8 us, 4096 x 4096 5.0 -> 4.0 us.
-template <int RT, int XR, int SP>
+template <int RT, int XR, bool SP>
 struct Tile {
   static constexpr int kRT = RT;
   static constexpr int kR = 16 * RT;
   static constexpr int kXR = XR;
   static constexpr int kTT = XR > 16 ? 2 : 1;                  // 16-token MFMA tiles
-  static constexpr bool kScPre = SP > 0;
+  static constexpr bool kScPre = SP;
   static constexpr int kSB = (kScPre && XR <= 2) ? 4 : (RT == 1 && XR <= 16) ? 2 : 1;  // NF4 blocks per stage
   static constexpr int kWBytes = kR * kSB * 32 < 1024 ? 1024 : kR * kSB * 32;
   static constexpr int kWDma = kWBytes / 1024;
@@ -56,8 +55,11 @@ struct Tile {
   static constexpr int kScBytes = kScPre ? 0 : 256;  // one dword copy: kR * kSB scales used
   static constexpr int kStage = kWBytes + kXBytes + kScBytes;
   static constexpr int kDma = kWDma + kXDma + (kScPre ? 0 : 1);  // copies per stage
-  // Tile<1, 8>: two workgroups per CU in LDS; Tile<1, 2>: 4-block stages.
-  static constexpr int kDepth = (SP == 2 || (RT == 1 && (XR == 8 || (kScPre && XR <= 2)))) ? 2 : 3;
+  // Scales in LDS: two stages, both streaming (against three: north-star
+  // B = 64 18.1 -> 17.8 us, B = 32 16.5 -> 16.1 us, c3 B = 64 gate/up
+  // 85.4 -> 81.1 us). Per-stage scales: three stages (Tile<1, 8>: two, for
+  // two workgroups per CU in LDS).
+  static constexpr int kDepth = (SP || (RT == 1 && XR == 8)) ? 2 : 3;
   static_assert(kR * kSB * 32 <= kWBytes && (kScPre || kR * kSB <= 64), "stage sizes");
   static_assert(kDma * (kDepth - 1) < 64, "vmcnt range");
 };
@@ -1054,7 +1056,7 @@ __device__ __forceinline__ void issue_scales(const GemvParams& p, char* area, in
 template <int RT, int XR>
 constexpr int kMinWavesPerSimd = (RT == 1 && XR <= 8) ? 4 : 2;
 
-template <int RT, int XR, bool kExact, bool kLora, bool kResidual, int kSP>
+template <int RT, int XR, bool kExact, bool kLora, bool kResidual, bool kSP>
 __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv_kernel(GemvParams p) {
   using TL = Tile<RT, XR, kSP>;
   constexpr int TT = TL::kTT;
@@ -1405,41 +1407,30 @@ int64_t static_lds_of(K fn, int64_t& cache) {
 
 // Launches the variant with the block scales in LDS (each contraction wave's
 // area in dynamic LDS, 16 trailing bytes: the last area's stage reads may run
-// up to 3 floats past it) when its static LDS and the areas fit, else, for
-// the tiles with three-deep rings, the same with a two-deep ring (the 32-row
-// tile at K = 12288), else the variant that stages the scales with the
-// weights (very long K).
+// up to 3 floats past it) when its static LDS and the areas fit, else the
+// variant that stages the scales with the weights (very long K).
 template <int RT, int XR, bool kExact, bool kLora>
 int launch_scaled(dim3 grid, hipStream_t s, GemvParams p) {
   constexpr int kBase = kLora ? kWaves - 1 : kWaves;
   const ScaleArea a = scale_area(p.k >> 6, kBase, 16 * RT);
   const int64_t dyn = int64_t(kBase) * a.bytes + 16;
-  auto fits = [&](int64_t st) { return st >= 0 && st + dyn <= kLdsBytes; };
-  static int64_t lds1 = -1, lds2 = -1;
-  auto fn1 = nf4_gemv_kernel<RT, XR, kExact, kLora, false, 1>;
-  if (fits(static_lds_of(fn1, lds1))) {
+  static int64_t static_lds = -1;
+  auto fn = nf4_gemv_kernel<RT, XR, kExact, kLora, false, true>;
+  const int64_t st = static_lds_of(fn, static_lds);
+  if (st >= 0 && st + dyn <= kLdsBytes) {
     p.sc_stride = a.stride;
     p.sc_bytes = a.bytes;
-    hipLaunchKernelGGL(fn1, grid, dim3(kThreads), size_t(dyn), s, p);
-    return kOk;
+    hipLaunchKernelGGL(fn, grid, dim3(kThreads), size_t(dyn), s, p);
+  } else {
+    hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, kExact, kLora, false, false>), grid, dim3(kThreads), 0, s, p);
   }
-  if constexpr (Tile<RT, XR, 1>::kDepth > 2) {
-    auto fn2 = nf4_gemv_kernel<RT, XR, kExact, kLora, false, 2>;
-    if (fits(static_lds_of(fn2, lds2))) {
-      p.sc_stride = a.stride;
-      p.sc_bytes = a.bytes;
-      hipLaunchKernelGGL(fn2, grid, dim3(kThreads), size_t(dyn), s, p);
-      return kOk;
-    }
-  }
-  hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, kExact, kLora, false, 0>), grid, dim3(kThreads), 0, s, p);
   return kOk;
 }
 
 template <int RT, int XR>
 int launch_tile(bool exact, bool lora, bool residual, dim3 grid, hipStream_t s, const GemvParams& p) {
   if (residual) {
-    hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, true, true, 0>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, false, true, true, false>), grid, dim3(kThreads), 0, s, p);
     return kOk;
   }
   if (lora) return exact ? launch_scaled<RT, XR, true, true>(grid, s, p) : launch_scaled<RT, XR, false, true>(grid, s, p);
