@@ -24,8 +24,10 @@
 // grid. The segment's z rows are staged in LDS as bf16, zero past the rank;
 // each wave contracts 16-column tiles of B_g (A operand, one 16-byte row
 // fragment per lane) with the staged z (B operand) over ceil(r / 32) MFMA
-// steps, so a lane ends with four consecutive columns of one token. Columns
-// of a tile that fall in another slice are masked out of that slice's MFMA.
+// steps, so a lane ends with four consecutive columns of one token (read and
+// written as one 8-byte access when y's rows are 8-byte aligned and the width
+// is a multiple of 4). Columns of a tile that fall in another slice are masked
+// out of that slice's MFMA; the slice bounds are read once per workgroup.
 #include <algorithm>
 
 #include "call_epoch.h"
@@ -274,6 +276,7 @@ struct ExpandArgs {
   int slices;
   int capacity;   // z row = slices * capacity
   int64_t y_stride;
+  int y_vec;      // y rows 8-byte aligned and n % 4 == 0: 4 columns per load/store
 };
 
 // Raw B values k .. k + 7 of one row (stride st; k a multiple of 8), loaded
@@ -314,6 +317,10 @@ __global__ __launch_bounds__(64 * kWaves) void row_expand_kernel(ExpandArgs p) {
   const int c = lane & 15;
   const int kg = lane >> 4;
   const int chunks = (p.n + kCols - 1) / kCols;
+  // Slice bounds (slices + 1 of them), read once ahead of every item.
+  int so[kMaxSlices + 1];
+#pragma unroll
+  for (int i = 0; i <= kMaxSlices; ++i) so[i] = i <= p.slices ? p.slice_offsets[i] : p.n;
   for (int item = blockIdx.x; item < p.segments * chunks; item += gridDim.x) {
     const int seg = item / chunks;
     const int n_base = (item - seg * chunks) * kCols;
@@ -344,8 +351,16 @@ __global__ __launch_bounds__(64 * kWaves) void row_expand_kernel(ExpandArgs p) {
       const uint16_t* row = p.b + boff + int64_t(min(n0 + c, p.n - 1)) * st;
       bf[tt][0] = b_load(row, st, 8 * kg);
       if (ksteps > 1) bf[tt][1] = b_load(row, st, 32 + 8 * kg);
+      if (p.y_vec) {
+        const uint2 q = *reinterpret_cast<const uint2*>(yrow + min(n0 + 4 * kg, p.n - 4));
+        yv[tt][0] = uint16_t(q.x);
+        yv[tt][1] = uint16_t(q.x >> 16);
+        yv[tt][2] = uint16_t(q.y);
+        yv[tt][3] = uint16_t(q.y >> 16);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) yv[tt][e] = yrow[min(n0 + 4 * kg + e, p.n - 1)];
+        for (int e = 0; e < 4; ++e) yv[tt][e] = yrow[min(n0 + 4 * kg + e, p.n - 1)];
+      }
     }
     const int total = p.slices * kMaxSegment << kbits;
     const int64_t zrow = int64_t(p.slices) * p.capacity;
@@ -378,15 +393,19 @@ __global__ __launch_bounds__(64 * kWaves) void row_expand_kernel(ExpandArgs p) {
     for (int tt = 0; tt < kTilesPerWave; ++tt) {
       const int n0 = n_base + (wave * kTilesPerWave + tt) * 16;
       if (n0 >= p.n) break;
-      // Slices touching columns n0 .. n0 + 15.
-      int s_lo = 0;
-      while (s_lo + 1 < p.slices && p.slice_offsets[s_lo + 1] <= n0) ++s_lo;
-      int s_hi = s_lo;
-      while (s_hi + 1 < p.slices && p.slice_offsets[s_hi + 1] < n0 + 16) ++s_hi;
+      // Slices touching columns n0 .. n0 + 15: s_lo .. s_hi.
+      int s_lo = 0, s_hi = 0;
+#pragma unroll
+      for (int i = 1; i < kMaxSlices; ++i) {
+        s_lo += (i < p.slices && so[i] <= n0) ? 1 : 0;
+        s_hi += (i < p.slices && so[i] < n0 + 16) ? 1 : 0;
+      }
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int s = s_lo; s <= s_hi; ++s) {
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) {
+        if (s < s_lo || s > s_hi) continue;
         const int n = n0 + c;  // this lane's B row
-        const bool mine = n >= p.slice_offsets[s] && n < p.slice_offsets[s + 1];
+        const bool mine = n >= so[s] && n < so[s + 1];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           if (h < ksteps) {
@@ -398,10 +417,16 @@ __global__ __launch_bounds__(64 * kWaves) void row_expand_kernel(ExpandArgs p) {
       // acc[e] = delta sum for column n0 + 4 kg + e of token c.
       if (c < count) {
         uint16_t* yrow = p.y + int64_t(my_token) * p.y_stride;
+        uint32_t o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int n = n0 + 4 * kg + e;
-          if (n < p.n) yrow[n] = uint16_t(f32_to_bf16(bf16_to_f32(yv[tt][e]) + round_bf16(acc[e] * scale)));
+        for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(bf16_to_f32(yv[tt][e]) + round_bf16(acc[e] * scale));
+        if (p.y_vec) {
+          if (n0 + 4 * kg < p.n)
+            *reinterpret_cast<uint2*>(yrow + n0 + 4 * kg) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n0 + 4 * kg + e < p.n) yrow[n0 + 4 * kg + e] = uint16_t(o[e]);
         }
       }
     }
@@ -530,7 +555,8 @@ extern "C" int lf_row_expand(const uint16_t* z, const uint16_t* b, const int64_t
   LF_REQUIRE(segments >= 0 && segments * ((out_width + 255) / 64) < (int64_t(1) << 31), "segment work count out of range");
   if (segments == 0) return lf::kOk;
   lf::ExpandArgs p{z, b, b_offsets, b_strides, y, segment_indptr, segment_slots, token_indices, ranks, scales,
-                   slice_offsets, segment_count, int(segments), int(out_width), int(num_slices), int(capacity), y_stride};
+                   slice_offsets, segment_count, int(segments), int(out_width), int(num_slices), int(capacity), y_stride,
+                   (out_width % 4 == 0 && y_stride % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0) ? 1 : 0};
   auto s = static_cast<hipStream_t>(stream);
   if (threads == 256)
     hipLaunchKernelGGL(lf::row_expand_kernel<4>, dim3(blocks), dim3(256), 0, s, p);
