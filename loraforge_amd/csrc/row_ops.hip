@@ -26,8 +26,10 @@
 // fragment per lane) with the staged z (B operand) over ceil(r / 32) MFMA
 // steps, so a lane ends with four consecutive columns of one token (read and
 // written as one 8-byte access when y's rows are 8-byte aligned and the width
-// is a multiple of 4). Columns of a tile that fall in another slice are masked
-// out of that slice's MFMA; the slice bounds are read once per workgroup.
+// is a multiple of 4; z values are staged 4 per 8-byte load when z's rows are
+// 8-byte aligned and the slot's rank is a multiple of 4). Columns of a tile
+// that fall in another slice are masked out of that slice's MFMA; the slice
+// bounds are read once per workgroup.
 #include <algorithm>
 
 #include "call_epoch.h"
@@ -277,6 +279,7 @@ struct ExpandArgs {
   int capacity;   // z row = slices * capacity
   int64_t y_stride;
   int y_vec;      // y rows 8-byte aligned and n % 4 == 0: 4 columns per load/store
+  int z_vec;      // z rows 8-byte aligned: a slot of rank % 4 == 0 stages 4 z values per load
 };
 
 // Raw B values k .. k + 7 of one row (stride st; k a multiple of 8), loaded
@@ -364,16 +367,31 @@ __global__ __launch_bounds__(64 * kWaves) void row_expand_kernel(ExpandArgs p) {
     }
     const int total = p.slices * kMaxSegment << kbits;
     const int64_t zrow = int64_t(p.slices) * p.capacity;
+    const bool zq_ok = p.z_vec && (r & 3) == 0;  // uniform
     uint16_t zv[kPer];
+    uint2 zq[kPer / 4];
+    if (zq_ok) {
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = tid + j * 64 * kWaves;
-      const int k = e & ((1 << kbits) - 1);
-      const int i = (e >> kbits) & (kMaxSegment - 1);
-      const int s = e >> (kbits + 4);
-      const int tok = __shfl(my_token, i, 64);  // lane i holds token i of the segment
-      const bool in = e < total && k < r;
-      zv[j] = p.z[tok * zrow + (in ? s * r + k : 0)];
+      for (int j = 0; j < kPer / 4; ++j) {
+        const int e = (tid + j * 64 * kWaves) * 4;  // first of four consecutive k
+        const int k = e & ((1 << kbits) - 1);
+        const int i = (e >> kbits) & (kMaxSegment - 1);
+        const int s = e >> (kbits + 4);
+        const int tok = __shfl(my_token, i, 64);  // lane i holds token i of the segment
+        const bool in = e < total && k < r;
+        zq[j] = *reinterpret_cast<const uint2*>(p.z + tok * zrow + (in ? s * r + k : 0));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int e = tid + j * 64 * kWaves;
+        const int k = e & ((1 << kbits) - 1);
+        const int i = (e >> kbits) & (kMaxSegment - 1);
+        const int s = e >> (kbits + 4);
+        const int tok = __shfl(my_token, i, 64);
+        const bool in = e < total && k < r;
+        zv[j] = p.z[tok * zrow + (in ? s * r + k : 0)];
+      }
     }
 #pragma unroll
     for (int tt = 0; tt < kTilesPerWave; ++tt) {
@@ -381,12 +399,23 @@ __global__ __launch_bounds__(64 * kWaves) void row_expand_kernel(ExpandArgs p) {
       bf[tt][1] = ksteps > 1 ? b_mask(bf[tt][1], st, r, 32 + 8 * kg) : make_uint4(0, 0, 0, 0);
     }
     __syncthreads();  // the previous item is done reading the staged z
+    if (zq_ok) {
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = tid + j * 64 * kWaves;
-      const int k = e & ((1 << kbits) - 1);
-      const int i = (e >> kbits) & (kMaxSegment - 1);
-      if (e < total) zs[e >> (kbits + 4)][i][k] = (i < count && k < r) ? zv[j] : uint16_t(0);
+      for (int j = 0; j < kPer / 4; ++j) {
+        const int e = (tid + j * 64 * kWaves) * 4;
+        const int k = e & ((1 << kbits) - 1);
+        const int i = (e >> kbits) & (kMaxSegment - 1);
+        if (e < total)
+          *reinterpret_cast<uint2*>(&zs[e >> (kbits + 4)][i][k]) = (i < count && k < r) ? zq[j] : make_uint2(0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int e = tid + j * 64 * kWaves;
+        const int k = e & ((1 << kbits) - 1);
+        const int i = (e >> kbits) & (kMaxSegment - 1);
+        if (e < total) zs[e >> (kbits + 4)][i][k] = (i < count && k < r) ? zv[j] : uint16_t(0);
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -556,7 +585,8 @@ extern "C" int lf_row_expand(const uint16_t* z, const uint16_t* b, const int64_t
   if (segments == 0) return lf::kOk;
   lf::ExpandArgs p{z, b, b_offsets, b_strides, y, segment_indptr, segment_slots, token_indices, ranks, scales,
                    slice_offsets, segment_count, int(segments), int(out_width), int(num_slices), int(capacity), y_stride,
-                   (out_width % 4 == 0 && y_stride % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0) ? 1 : 0};
+                   (out_width % 4 == 0 && y_stride % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0) ? 1 : 0,
+                   (capacity * num_slices % 4 == 0 && reinterpret_cast<uintptr_t>(z) % 8 == 0) ? 1 : 0};
   auto s = static_cast<hipStream_t>(stream);
   if (threads == 256)
     hipLaunchKernelGGL(lf::row_expand_kernel<4>, dim3(blocks), dim3(256), 0, s, p);
