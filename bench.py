@@ -715,4 +715,17 @@ def main() -> int:
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    rc = main()
+    # The JSON line is out: end the process at once instead of tearing down
+    # torch's HIP state and the resident copies (which leaves it running for a
+    # while after the result is printed).
+    sys.stdout.flush()
+    sys.stderr.flush()
+    try:
+        import torch
+
+        if torch.cuda.is_initialized():
+            torch.cuda.synchronize()
+    except Exception:  # noqa: BLE001 - best effort before exiting
+        pass
+    os._exit(rc)

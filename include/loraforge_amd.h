@@ -23,7 +23,9 @@
 extern "C" {
 #endif
 
-#define LF_ABI_VERSION 1
+/* 2: lf_row_shrink gained num_adapters, workspace, workspace_bytes and flags,
+ * lf_row_expand gained segments (arguments inserted mid-list). */
+#define LF_ABI_VERSION 2
 #define LF_OK 0
 #define LF_EINVAL 1
 #define LF_EHIP 2
@@ -39,8 +41,9 @@ int lf_device_arch(int device, char* name, int capacity);
  * kernel ops/_nf4_kernels.py:44-61) behind dequantize_nf4 (ops/nf4.py:44).
  * out[e] = bf16_rne(code[nibble(e)] * scales[e / 64]); nibble(e) is the high
  * nibble of byte e/2 for even e, the low nibble for odd e.
- * numel = N*K, a positive multiple of 4096. qweight 4-byte aligned, out
- * 16-byte aligned.
+ * numel = N*K, a positive multiple of 4096. Any byte address for qweight and
+ * any 2-byte address for out (the reference accepts every contiguous tensor);
+ * qweight 4-byte aligned with out 16-byte aligned takes the vector path.
  * ------------------------------------------------------------------------ */
 int lf_nf4_dequant(const uint8_t* qweight, const float* scales, const float* code, uint16_t* out,
                    int64_t numel, void* stream);
@@ -212,9 +215,11 @@ int lf_lora_apply(const uint16_t* x, int64_t m, int64_t x_stride, int64_t n, int
  * device (held until the process ends), and problems whose
  * lf_nf4_lora_workspace_size exceeds it are rejected with LF_EINVAL. The
  * first call on a device clears the array on its stream and must not be
- * captured; later calls may be. It calls no allocator. Every call on a
- * device shares that device's array: calls that overlap in time on one GPU
- * race. */
+ * captured; it finishes the clear (synchronising its stream once) before
+ * returning, so later calls on any stream find the array cleared; later
+ * calls may be captured. It calls no allocator. Every call on a device
+ * shares that device's array: calls that overlap in time on one GPU race,
+ * so calls on different streams must be ordered by the caller (events). */
 #define LF_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
 int lf_nf4_lora_linear_noalloc(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* weight,
                                const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,

@@ -6,7 +6,10 @@
 // and writes 128 bytes. Each lane decodes one packed dword (8 elements) per
 // step and stores 16 bytes, so every load (256 B/wave) and store (1 KiB/wave)
 // instruction is fully coalesced. Four independent steps per lane keep
-// enough bytes in flight.
+// enough bytes in flight. Packed bytes at an address that is not 4-byte
+// aligned, or an output that is not 16-byte aligned (a contiguous view at an
+// odd offset, which the reference accepts), take the same kernel with byte
+// loads and 2-byte stores.
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
 
@@ -16,10 +19,37 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kSteps = 4;
 
-template <bool kDouble>
-__global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(const uint32_t* __restrict__ packed,
+// Packed dword w of the weight (bytes 4w..4w+3, little endian).
+template <bool kAligned>
+__device__ __forceinline__ uint32_t load_packed(const uint8_t* __restrict__ packed, int64_t w) {
+  if constexpr (kAligned) {
+    return reinterpret_cast<const uint32_t*>(packed)[w];
+  } else {
+    const uint8_t* p = packed + 4 * w;
+    return uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16) | (uint32_t(p[3]) << 24);
+  }
+}
+
+// Elements 8w..8w+7 of the output.
+template <bool kAligned>
+__device__ __forceinline__ void store_elements(uint16_t* __restrict__ out, int64_t w, uint4 v) {
+  if constexpr (kAligned) {
+    reinterpret_cast<uint4*>(out)[w] = v;
+  } else {
+    uint16_t* p = out + 8 * w;
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[2 * i] = uint16_t(words[i] & 0xffffu);
+      p[2 * i + 1] = uint16_t(words[i] >> 16);
+    }
+  }
+}
+
+template <bool kDouble, bool kAligned>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(const uint8_t* __restrict__ packed,
                                                                ScaleSource src, const float* __restrict__ code,
-                                                               uint4* __restrict__ out, int64_t ndwords) {
+                                                               uint16_t* __restrict__ out, int64_t ndwords) {
   __shared__ float table[16];
   __shared__ float code2[kDouble ? 256 : 1];
   // Packed bytes are requested first; the codebook is staged while they travel.
@@ -28,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(const uint32_t* _
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int64_t w = base + s * kThreads;
-    words[s] = w < ndwords ? packed[w] : 0u;
+    words[s] = w < ndwords ? load_packed<kAligned>(packed, w) : 0u;
   }
   const float offset = kDouble ? *src.offset : 0.0f;
   if (threadIdx.x < 16) table[threadIdx.x] = code[threadIdx.x];
@@ -40,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_kernel(const uint32_t* _
     if (w < ndwords) {
       // 8 elements per dword, 64 per block: block = w / 8.
       const float scale = block_scale(src, w >> 3, code2, offset);
-      out[w] = decode_dword(words[s], scale, table);
+      store_elements<kAligned>(out, w, decode_dword(words[s], scale, table));
     }
   }
 }
@@ -62,18 +92,18 @@ int launch_dequant(const uint8_t* qweight, const ScaleSource& src, const float* 
   LF_REQUIRE(numel > 0 && numel % (kNf4Block * kNf4Block) == 0,
              "element count must be a positive multiple of 4096");
   LF_REQUIRE(qweight && code && out, "null pointer argument");
-  LF_REQUIRE(aligned16(out) && (reinterpret_cast<uintptr_t>(qweight) & 3u) == 0,
-             "packed bytes must be 4-byte aligned and out 16-byte aligned");
+  LF_REQUIRE((reinterpret_cast<uintptr_t>(out) & 1u) == 0, "out must be 2-byte aligned (bf16)");
   const int64_t ndwords = numel / 8;
   const int64_t grid = (ndwords + kThreads * kSteps - 1) / (kThreads * kSteps);
   LF_REQUIRE(grid < (int64_t(1) << 31), "tensor too large");
   auto s = static_cast<hipStream_t>(stream);
-  const auto* packed = reinterpret_cast<const uint32_t*>(qweight);
-  auto* o = reinterpret_cast<uint4*>(out);
+  const bool vec = aligned16(out) && (reinterpret_cast<uintptr_t>(qweight) & 3u) == 0;
   if (src.scales) {
-    hipLaunchKernelGGL(nf4_dequant_kernel<false>, dim3(grid), dim3(kThreads), 0, s, packed, src, code, o, ndwords);
+    auto k = vec ? nf4_dequant_kernel<false, true> : nf4_dequant_kernel<false, false>;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, qweight, src, code, out, ndwords);
   } else {
-    hipLaunchKernelGGL(nf4_dequant_kernel<true>, dim3(grid), dim3(kThreads), 0, s, packed, src, code, o, ndwords);
+    auto k = vec ? nf4_dequant_kernel<true, true> : nf4_dequant_kernel<true, false>;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, qweight, src, code, out, ndwords);
   }
   LF_HIP(hipGetLastError());
   return kOk;

@@ -10,7 +10,9 @@
 // what the kernels receive.
 //
 // The array is cleared once per device (a fill kernel on the first call's
-// stream, which must therefore not be capturing); afterwards the kernels'
+// stream, which must therefore not be capturing, waited for before the
+// pointer is published, so a later call on any other stream finds the array
+// cleared); afterwards the kernels'
 // call-epoch protocol keeps it valid (entries are tagged with the call that
 // wrote them, arrival counters return to zero at the end of every call).
 // Every call on a device shares that device's array and leaves its contents
@@ -38,7 +40,7 @@ __global__ void fill_zero_kernel(uint4* dst, int64_t n16) {
 }
 
 // This device's copy of the scratch array (looked up and cleared on the
-// first call on the device, on `stream`).
+// first call on the device, on `stream`, which is synchronised once).
 int device_scratch(hipStream_t stream, void** out) {
   int dev = -1;
   LF_HIP(hipGetDevice(&dev));
@@ -54,6 +56,9 @@ int device_scratch(hipStream_t stream, void** out) {
     LF_REQUIRE(ptr != nullptr && aligned16(ptr), "scratch symbol has no usable device address");
     hipLaunchKernelGGL(fill_zero_kernel, dim3(256), dim3(256), 0, stream, static_cast<uint4*>(ptr), kScratchBytes / 16);
     LF_HIP(hipGetLastError());
+    // Calls on other streams are not ordered after this fill: finish it
+    // before any call can see the pointer.
+    LF_HIP(hipStreamSynchronize(stream));
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];

@@ -342,8 +342,10 @@ def nf4_lora_linear(
         if m > 32:
             from .activation import silu_mul
 
-            if out is not None and (out.dtype != torch.bfloat16 or out.shape != (*lead, width) or out.stride(-1) != 1):
-                raise ValueError("out must be bf16 [..., N/2] on the input device")
+            if out is not None:
+                if out.dtype != torch.bfloat16 or out.shape != (*lead, width) or out.device != device or out.stride(-1) != 1:
+                    raise ValueError("out must be bf16 [..., N/2] on the input device")
+                distinct_output(out, (x, qweight, bias))
             gate_up = nf4_lora_linear(
                 x2, qweight, state, scales=scales, bias=bias, lora=lora, workspace=workspace, exact=exact, plan=plan
             )

@@ -230,8 +230,6 @@ def dequantize_nf4(qweight, scales, code, shape: tuple[int, int], *, out=None):
         or any(not t.is_contiguous() or t.requires_grad for t in (qweight, scales, code))
     ):
         raise ValueError("requires contiguous uint8 bytes, FP32 block64 scales and a 16-entry codebook")
-    if qweight.data_ptr() % 4:
-        raise ValueError("packed bytes must be 4-byte aligned")
     if out is not None:
         if (
             not isinstance(out, torch.Tensor)
@@ -248,8 +246,6 @@ def dequantize_nf4(qweight, scales, code, shape: tuple[int, int], *, out=None):
     with torch.cuda.device(device):
         if out is None:
             out = torch.empty(shape, device=device, dtype=torch.bfloat16)
-        if out.data_ptr() % 16:
-            raise ValueError("out must be 16-byte aligned")
         _lib.check(
             lib.lf_nf4_dequant(
                 qweight.data_ptr(), scales.data_ptr(), code.data_ptr(), out.data_ptr(), size, _lib.stream_of(device)

@@ -125,6 +125,13 @@ def plan_regions(catalog: dict, name: str, layer: int, width: int) -> tuple[dict
     return regions, end
 
 
+def _capturing(device) -> bool:
+    """Whether the current stream of a CUDA/ROCm device is being captured into a graph."""
+    import torch
+
+    return device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
+
 class RetainedLayout:
     """Compact B regions and fixed per-slot metadata for one fused projection of an SGLang pool.
 
@@ -164,6 +171,7 @@ class RetainedLayout:
         self.has_unsupported = any(k > 64 for k in ks)
         self.max_rank = max([1] + [min(64, region.bucket) for region in self.regions.values()])
         self.loaded: dict = {}
+        self._bounds: dict = {}  # slice_offsets tuple -> int32 device bounds (built once, eagerly)
 
     def validate_load(self, path, checkpoint_rank) -> None:
         if path is None:
@@ -207,6 +215,9 @@ class RetainedLayout:
         ``batch_info.scalings``); ``slice_offsets``: the output partition of
         the fused projection (default: ``slices`` equal parts of the width).
         Slots whose rank exceeds 64 are served by another path and are refused.
+        The device copy of each distinct ``slice_offsets`` is built on its first
+        (eager) call and reused, so later calls copy nothing from the host and
+        may be captured; a partition first seen under capture is refused.
         """
         import torch
 
@@ -220,9 +231,14 @@ class RetainedLayout:
             if width % self.slices:
                 raise ValueError("pass slice_offsets: the width does not split evenly into slices")
             slice_offsets = [s * (width // self.slices) for s in range(self.slices + 1)]
-        bounds = torch.as_tensor(slice_offsets, dtype=torch.int32).to(self.b.device)
-        if bounds.numel() != self.slices + 1:
+        key = tuple(int(v) for v in slice_offsets)
+        if len(key) != self.slices + 1:
             raise ValueError("slice_offsets must have slices + 1 entries")
+        bounds = self._bounds.get(key)
+        if bounds is None:
+            if _capturing(self.b.device):
+                raise RuntimeError("warm each projection's slice_offsets with an eager call before capturing")
+            bounds = self._bounds[key] = torch.tensor(key, dtype=torch.int32, device=self.b.device)
         return LoraBatch(
             self.a.view(-1),
             self.a_offsets,

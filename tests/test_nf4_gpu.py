@@ -113,3 +113,34 @@ def test_output_cannot_alias_packed_input_storage(device):
     code = torch.zeros(16, device=device, dtype=torch.float32)
     with pytest.raises(ValueError, match="alias"):
         dequantize_nf4(packed, scales, code, (64, 64), out=out)
+
+
+@pytest.mark.parametrize("q_offset,out_offset", [(1, 4), (3, 1), (4, 4), (0, 3)])
+def test_views_at_unaligned_offsets(q_offset, out_offset, device):
+    """Contiguous views at any offset are accepted, as the reference accepts them
+    (``ops/nf4.py:76-104`` checks dtype, size and contiguity only): qweight at a byte
+    offset, out at an element offset (2-byte steps), both bit-exact, for fp32 and nested
+    scales."""
+    shape = (128, 192)
+    rng = np.random.default_rng(733)
+    w = onf4.bf16_to_f32(_cases.bf16(rng.standard_normal(shape) * 0.1))
+    state = onf4.quantize(w, double_quant=True)
+    expect = onf4.dequantize(state["qweight"], state["scales"], shape)
+    q, st = _state_tensors(state, device)
+    scales = prepare_scales(st)
+    packed = torch.zeros(q.numel() + 16, dtype=torch.uint8, device=device)
+    qv = packed[q_offset : q_offset + q.numel()]
+    qv.copy_(q)
+    backing = torch.zeros(shape[0] * shape[1] + 16, dtype=torch.bfloat16, device=device)
+    out = backing[out_offset : out_offset + shape[0] * shape[1]].view(shape)
+    print(f"[nf4] unaligned views q+{q_offset} out+{out_offset}", flush=True)
+    assert dequantize_nf4(qv, scales, st.code, shape, out=out) is out
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(out), expect)
+    assert not backing[:out_offset].any() and not backing[out_offset + shape[0] * shape[1] :].any()
+    assert np.array_equal(_bits(dequantize_nf4_nested(qv, st, out=torch.empty(shape, dtype=torch.bfloat16, device=device))), expect)
+    nested_out = backing[out_offset : out_offset + shape[0] * shape[1]].view(shape)
+    nested_out.zero_()
+    dequantize_nf4_nested(qv, st, out=nested_out)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(nested_out), expect)

@@ -377,6 +377,20 @@ def test_retained_layout_feeds_the_fused_batch():
     np.testing.assert_allclose(onf4_f32(got), onf4_f32(want), rtol=1e-2, atol=1e-2)
     with pytest.raises(ValueError, match="slice_offsets"):
         layout.lora_batch(torch.from_numpy(route), scales, slice_offsets=[0, 24])
+    # The device bounds of a partition are built once and reused (no host copy per call);
+    # a partition first seen under graph capture is refused.
+    again = layout.lora_batch(torch.from_numpy(route), scales)
+    assert again.slice_offsets is batch.slice_offsets
+    from loraforge_amd.runtime import retained
+
+    capturing = retained._capturing
+    try:
+        retained._capturing = lambda device: True
+        assert layout.lora_batch(torch.from_numpy(route), scales).slice_offsets is batch.slice_offsets
+        with pytest.raises(RuntimeError, match="before capturing"):
+            layout.lora_batch(torch.from_numpy(route), scales, slice_offsets=[0, 8, 24])
+    finally:
+        retained._capturing = capturing
 
 
 def test_retained_layout_refuses_wide_slots_in_the_fused_batch():

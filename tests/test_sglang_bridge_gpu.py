@@ -113,6 +113,42 @@ def test_bridge_graph_replay_follows_new_metadata(weight, device):
         close(bits(out), expected(x_bits, w_bits, batch, routes, 1024))
 
 
+def test_bridge_graph_replay_over_retained_layout(weight, device):
+    """A graph captured over a RetainedLayout (after one eager call built its slice bounds)
+    replays new routing written into the same batch_info buffers."""
+    w_bits, q, state = weight
+    tokens = 24
+    rng = np.random.default_rng(7)
+    layout = retained_pool(rng, device)
+    info, routes = random_info(rng, tokens, 6, padded=3, device=device)
+    info.scalings = torch.tensor([2.0, 1.0, 0.5, 1.5, 0.25, 1.0], device=device)
+    x_bits = _cases.bf16(rng.standard_normal((tokens, 512)))
+    x = t16(x_bits, device)
+    slots_buf = torch.empty(tokens, dtype=torch.int32, device=device)
+    out = torch.empty(tokens, 1024, dtype=torch.bfloat16, device=device)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        apply_nf4_lora(x, q, state, info, layout, out=out, token_slots=slots_buf)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            apply_nf4_lora(x, q, state, info, layout, out=out, token_slots=slots_buf)
+    torch.cuda.synchronize()
+    batch = lora_batch_from_batch_info(info, layout, tokens=tokens)
+    for rep in range(3):
+        fresh, routes = random_info(np.random.default_rng(300 + rep), tokens, 6, padded=3,
+                                    segments=info.num_segments, device=device)
+        info.seg_indptr.copy_(fresh.seg_indptr)
+        info.weight_indices.copy_(fresh.weight_indices)
+        info.permutation.copy_(fresh.permutation)
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(slots_buf.cpu().numpy(), routes)
+        close(bits(out), expected(x_bits, w_bits, batch, routes, 1024))
+
+
 @pytest.mark.parametrize("tokens", [5, 64, 150])
 def test_bridge_lora_only_update(tokens, device):
     """apply_lora: SGLang's batch over a retained layout, y (the caller's base output) updated in place."""

@@ -165,6 +165,23 @@ def test_fused_swiglu_output_equals_the_separate_chain(m, with_lora, device):
     assert_activation(bits(h), linear.silu_mul(bits(gu)[:, :inter], bits(gu)[:, inter:]))
 
 
+@pytest.mark.parametrize("m", [16, 48])
+def test_fused_swiglu_checks_out_like_the_linear(m, device):
+    """swiglu=True checks out for every batch size the same way (device and storage of the
+    inputs), also where the library runs the linear and the activation as two launches."""
+    inter = 256
+    case = _cases.fused_case(m, 2 * inter, 512, ranks=(8,), slices=2, bounds=[0, inter, 2 * inter], seed=890 + m)
+    x, q, st, lora, _ = to_device(case, device)
+    with pytest.raises(ValueError, match="input device"):
+        nf4_lora_linear(x, q, st, lora=lora, swiglu=True, out=torch.empty(m, inter, dtype=torch.bfloat16))
+    backing = torch.zeros(m * (512 + inter), dtype=torch.bfloat16, device=device)
+    xs = backing[: m * 512].view(m, 512)
+    xs.copy_(x)
+    with pytest.raises(ValueError, match="share storage"):
+        nf4_lora_linear(xs, q, st, lora=lora, swiglu=True, out=backing[m * 512 :].view(m, inter))
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("m", [1, 8, 64])
 def test_c3_gate_up_swiglu_fused_full_size(m, device):
     """c3's gate/up [2 x 12288, 4096] (double quant, 16 rank-8 adapters) with the SwiGLU in the epilogue."""

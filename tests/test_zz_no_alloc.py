@@ -46,6 +46,35 @@ def _subset(case, m):
     return sub
 
 
+def test_noalloc_first_calls_on_two_streams(device):
+    """The device's first allocation-free call runs on stream A and the next on stream B,
+    issued right after the first returned with no host synchronisation between them (B only
+    waits for A's work, as calls sharing the scratch must be ordered): the second must find
+    the scratch cleared (first in this file, so in a fresh process it is the device's first
+    call)."""
+    case = _cases.fused_case(24, 1024, 2048, ranks=(16, 8, 32), seed=86)
+    x, q, st, lora, _ = to_device(case, device)
+    expect = _cases.fused_expected(case)
+    ws = torch.zeros(_lib.library().lf_nf4_lora_workspace_size(24, 1024, 2048, 1, lora.max_rank), dtype=torch.uint8, device=device)
+    ref = torch.empty(24, 1024, dtype=torch.bfloat16, device=device)
+    _call("workspace", x, q, st, lora, ref, ws=ws)
+    torch.cuda.synchronize()
+    outs = [torch.full((24, 1024), 3.0, dtype=torch.bfloat16, device=device) for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    print("[noalloc] first call on stream A, second on stream B", flush=True)
+    with torch.cuda.stream(streams[0]):
+        _call("noalloc", x, q, st, lora, outs[0])
+    streams[1].wait_stream(streams[0])
+    with torch.cuda.stream(streams[1]):
+        _call("noalloc", x, q, st, lora, outs[1])
+    torch.cuda.synchronize()
+    for out in outs:
+        assert torch.equal(out, ref)
+        close(bits(out), expect)
+
+
 @pytest.mark.parametrize(
     "shape",
     [
