@@ -44,7 +44,7 @@ HIP_FLAGS = [
 # Sources whose kernels must not use scratch: the decode and prefill kernels
 # issue loads the compiler does not track (waited for explicitly), and a
 # register spill of such a result would store it before the load returned.
-NO_SCRATCH = {"nf4_gemv.hip", "nf4_lora_prefill.hip", "row_ops.hip"}
+NO_SCRATCH = {"nf4_gemv.hip", "nf4_decode_wide.hip", "nf4_lora_prefill.hip", "row_ops.hip"}
 
 
 def hipcc() -> str:

@@ -72,6 +72,13 @@ __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
 
+// One 32x32x16 bf16 MFMA step (layout checked on gfx950 against a CPU matmul):
+// lane l supplies a[l%32][8*(l/32) .. +8] and b[8*(l/32) .. +8][l%32];
+// acc[r] of lane l is c[8*(r/4) + 4*(l/32) + r%4][l%32].
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& acc) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 
 // Wave-wide fp32 sum (wave64) through cross-lane shuffles.

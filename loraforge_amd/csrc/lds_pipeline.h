@@ -79,4 +79,30 @@ __device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
 
 __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// A 16-byte global load into registers that the compiler does not track.
+// While direct LDS copies are in flight, the compiler waits for every
+// outstanding memory operation before using any tracked load result; the
+// kernels wait for these loads with an explicit vmcnt (loads complete in
+// issue order) and tie the result to that wait before its first use.
+__device__ __forceinline__ u32x4 global_load128_untracked(const void* ptr) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr) : "memory");
+  return v;
+}
+
+// The same for the lanes of `lanes` only (the others keep zero and issue no
+// memory request): the whole exec change stays inside the statement.
+__device__ __forceinline__ u32x4 global_load128_untracked_masked(const void* ptr, uint64_t lanes) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  uint64_t saved;
+  asm volatile(
+      "s_and_saveexec_b64 %1, %3\n\t"
+      "global_load_dwordx4 %0, %2, off\n\t"
+      "s_mov_b64 exec, %1"
+      : "+v"(v), "=&s"(saved)
+      : "v"(ptr), "s"(lanes)
+      : "memory", "exec");
+  return v;
+}
+
 }  // namespace lf

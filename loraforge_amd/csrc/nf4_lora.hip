@@ -17,7 +17,25 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
                             void* workspace, int64_t workspace_bytes, bool withhold, void* stream);
 int device_cus();
+bool decode_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora);
+int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
+                       const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
+                       bool exact, bool swiglu, bool withhold, void* stream);
 constexpr int64_t kDecodeMaxTokens = 64;
+
+// Whether the wide decode kernel (32 rows x 32 tokens per workgroup over the
+// whole K) serves M > 64 tokens faster than the prefill GEMM. Costs in us from
+// measured times on MI355X: a round of 256 wide workgroups takes about 4 us
+// per 4096 of K (its per-CU x and weight reads); a prefill round of 256 x 192
+// tiles about 85 us per 4096 of K.
+bool wide_cheaper(int64_t m, int64_t n, int64_t k) {
+  const int64_t cus = device_cus();
+  const int64_t wide_groups = ((n / 32 + 7) / 8) * 8 * ((m + 31) / 32);
+  const double wide_us = double((wide_groups + cus - 1) / cus) * 4.0 * double(k) / 4096.0;
+  const int64_t tiles = ((m + 255) / 256) * ((n + 191) / 192);
+  const double prefill_us = double((tiles + cus - 1) / cus) * 85.0 * double(k) / 4096.0;
+  return wide_us < prefill_us;
+}
 
 // Whether M > 64 tokens are served faster by the decode kernel over 64-token
 // chunks than by one prefill launch. The prefill GEMM runs 256 x 192 tiles,
@@ -38,6 +56,18 @@ bool decode_chunks_cheaper(int64_t m, int64_t n, int64_t k, bool lora) {
   const int64_t rounds = (tiles + cus - 1) / cus;
   const double prefill_us = double(rounds) * 85.0 * double(k) / 4096.0 + (lora ? 20.0 : 0.0);
   return double(chunks) * chunk_us < prefill_us;
+}
+// One decode launch of up to 64 tokens: the wide kernel above 32 tokens when
+// it takes the shape, else the narrow one (the kernel a direct call of these
+// rows would use, so each chunk of the chunked plan equals that call).
+int launch_decode(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
+                  const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
+                  bool exact, bool swiglu, bool withhold, void* stream) {
+  if (m > 32 && decode_wide_fits(m, w->n, w->k, lora))
+    return launch_decode_wide(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
+                              withhold, stream);
+  return launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
+                         withhold, stream);
 }
 }  // namespace lf
 
@@ -82,14 +112,21 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
     LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
   }
   const bool exact = (flags & LF_EXACT_WEIGHTS) != 0;
+  // Above 32 tokens: the wide decode kernel (one launch, base linear with or
+  // without LoRA and the SwiGLU output), unless the prefill GEMM is forced or
+  // cheaper, or the shape is outside the kernel's range.
+  if (m > 32 && w->scales && lf::decode_wide_fits(m, n, k, lora) && !(flags & LF_PLAN_PREFILL) &&
+      (m <= lf::kDecodeMaxTokens || (flags & LF_PLAN_DECODE_CHUNKS) || lf::wide_cheaper(m, n, k)))
+    return lf::launch_decode_wide(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact,
+                                  swiglu, withhold, stream);
   if (m <= lf::kDecodeMaxTokens) {
     // The decode kernel streams fp32 block scales (as the reference serves
     // decode from prepare_scales output): nested states go through
     // lf_nf4_prepare_scales_dq once per weight.
     LF_REQUIRE(w->scales != nullptr,
                "decode (M <= 64) takes fp32 block scales: build them with lf_nf4_prepare_scales_dq");
-    return lf::launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
-                               withhold, stream);
+    return lf::launch_decode(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
+                             withhold, stream);
   }
   bool chunked = false;
   if (flags & LF_PLAN_DECODE_CHUNKS) {
@@ -110,9 +147,9 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
       part = *lora;
       part.token_slots = lora->token_slots + t0;
     }
-    const int rc = lf::launch_nf4_gemv(x + t0 * x_stride, mc, x_stride, w, bias, lora ? &part : nullptr,
-                                       y + t0 * y_stride, y_stride, workspace, workspace_bytes, exact, false,
-                                       withhold, stream);
+    const int rc = lf::launch_decode(x + t0 * x_stride, mc, x_stride, w, bias, lora ? &part : nullptr,
+                                     y + t0 * y_stride, y_stride, workspace, workspace_bytes, exact, false, withhold,
+                                     stream);
     if (rc != lf::kOk) return rc;
   }
   return lf::kOk;
