@@ -24,8 +24,9 @@ extern "C" {
 #endif
 
 /* 2: lf_row_shrink gained num_adapters, workspace, workspace_bytes and flags,
- * lf_row_expand gained segments (arguments inserted mid-list). */
-#define LF_ABI_VERSION 2
+ * lf_row_expand gained segments (arguments inserted mid-list).
+ * 3: lf_lora gained num_slots (appended). */
+#define LF_ABI_VERSION 3
 #define LF_OK 0
 #define LF_EINVAL 1
 #define LF_EHIP 2
@@ -149,6 +150,12 @@ typedef struct lf_lora {
   const int32_t* slice_offsets; /* [num_slices+1] */
   int32_t num_slices;         /* 1..3 */
   int32_t max_rank;           /* 1..64 */
+  int32_t num_slots;          /* G, the entries of the per-slot arrays, or 0
+                                 when not given. When given, token slots >= G
+                                 run base only, and with G <= 256 the decode
+                                 kernel for 33..64 tokens requests the per-slot
+                                 arrays whole at its start, before it has read
+                                 the tokens' slots. */
 } lf_lora;
 
 /* Bytes of device workspace lf_nf4_lora_linear needs for this problem. The

@@ -24,7 +24,7 @@ LF_PLAN_DECODE_CHUNKS = 4
 LF_PLAN_PREFILL = 8
 LF_TEST_WITHHOLD_PARTIALS = 0x100
 NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _handle: ctypes.CDLL | None = None
@@ -63,6 +63,7 @@ class Lora(ctypes.Structure):
         ("slice_offsets", c_void_p),
         ("num_slices", c_int32),
         ("max_rank", c_int32),
+        ("num_slots", c_int32),
     ]
 
 

@@ -61,6 +61,7 @@ struct GemvParams {
   const int32_t* slice_offsets;
   int slices;
   int max_rank;
+  int num_slots;  // entries of the per-slot arrays (0: not given)
   int zw;         // z row width: slices * max_rank
   int units;      // shrink units: m * usplit * kz
   int kz;         // k-slices per token
@@ -137,7 +138,7 @@ __device__ __forceinline__ bool unit_of_slot(const GemvParams& p, int u, int g, 
   const int range = rest >> (31 - __builtin_clz(p.kz));  // kz is a power of two
   un.ks = rest - range * p.kz;
   const int ks = un.ks;
-  if (g < 0) return false;
+  if (g < 0 || (p.num_slots > 0 && g >= p.num_slots)) return false;
   const int r = sload(p.ranks, g);
   if (r <= 0 || r > p.max_rank) return false;
   un.j0 = range * p.urows;
@@ -360,6 +361,7 @@ struct TileMeta {
   int dstride[32];
   int64_t dboff[32];
   int start[33];  // z values the tile's tokens need (slices * r, 0 base only), exclusive prefix; start[32] = total
+  int bounds[4];  // slice_offsets[0 .. slices] (the wide kernel's copy for its base waves)
   int nd;
   int ready;  // set once the fields above are written (cleared at launch start)
 };
@@ -417,14 +419,28 @@ __device__ __forceinline__ uint4 b8_fix(const uint4& v, const B8& b) {
   return make_uint4(out[0], out[1], out[2], out[3]);
 }
 
+// z row stride in LDS (elements): a tile shape may set kZRow (a multiple
+// of 8, at least 192); otherwise 192 (three slices of 64).
+template <class TL, class = void>
+struct ZRow {
+  static constexpr int value = 192;
+};
+template <class TL>
+struct ZRow<TL, std::void_t<decltype(TL::kZRow)>> {
+  static constexpr int value = TL::kZRow;
+};
+
 // LDS of the LoRA stages, an array that never receives direct copies (so
-// stores into it do not wait for copies in flight): the tile metadata and z.
+// stores into it do not wait for copies in flight): the tile metadata and z
+// (token i's slice s at i * kZRow + 64 s).
 template <class TL>
 struct LoraLds {
   static constexpr int kMeta = 0;
-  static constexpr int kZ = 2048;  // z: [tile token][3 slices][64] bf16
-  static constexpr int kBytes = kZ + TL::kXR * 192 * 2;
+  static constexpr int kZ = 2048;  // z: [tile token][kZRow] bf16
+  static constexpr int kZRow = ZRow<TL>::value;
+  static constexpr int kBytes = kZ + TL::kXR * kZRow * 2;
   static_assert(sizeof(TileMeta) <= 2048, "tile metadata");
+  static_assert(kZRow >= 192 && kZRow % 8 == 0, "z rows hold three 64-value slices, 16-byte aligned");
 };
 
 // The LoRA wave, part 1a (before the workgroup's table barrier, while
@@ -443,7 +459,7 @@ struct TokenMeta {
 // g: token_slots[t0 + min(lane, mt - 1)], loaded by the caller.
 __device__ __forceinline__ TokenMeta token_meta(const GemvParams& p, int g, int mt, int lane) {
   TokenMeta m;
-  m.g = lane < mt ? g : -1;
+  m.g = lane < mt && (p.num_slots == 0 || g < p.num_slots) ? g : -1;
   const bool live = m.g >= 0;
   const void* fb = p.slice_offsets;
   m.r = *(live ? p.ranks + m.g : static_cast<const int32_t*>(fb));
@@ -451,6 +467,77 @@ __device__ __forceinline__ TokenMeta token_meta(const GemvParams& p, int g, int 
   m.scale = *(live ? p.lscales + m.g : static_cast<const float*>(fb));
   m.boff = *(live ? p.b_offsets + m.g : static_cast<const int64_t*>(fb));
   if (!live || m.r <= 0 || m.r > p.max_rank) {
+    m.g = -1;
+    m.r = 0;
+    m.stride = 1;
+    m.scale = 0.f;
+    m.boff = 0;
+  }
+  return m;
+}
+
+// The per-slot metadata of up to 256 slots in registers (lane l holds
+// slots l, l + 64, l + 128, l + 192), requested by a LoRA wave at its start:
+// these loads do not wait for the tile's token slots, so they can go out
+// before the workgroup's copies. Token metadata then comes from lane
+// shuffles (token_meta_from).
+constexpr int kSlotTableMax = 256;
+struct SlotTable {
+  int r[4];
+  int stride[4];
+  float scale[4];
+  int64_t boff[4];
+};
+
+__device__ __forceinline__ bool slot_table_usable(const GemvParams& p) {
+  return p.num_slots > 0 && p.num_slots <= kSlotTableMax;
+}
+
+__device__ __forceinline__ void slot_table_load(const GemvParams& p, int lane, SlotTable& t) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    t.r[c] = 0;
+    t.stride[c] = 1;
+    t.scale[c] = 0.f;
+    t.boff[c] = 0;
+    if (64 * c < p.num_slots) {  // uniform
+      const int s = min(64 * c + lane, p.num_slots - 1);
+      t.r[c] = p.ranks[s];
+      t.stride[c] = p.b_strides[s];
+      t.scale[c] = p.lscales[s];
+      t.boff[c] = p.b_offsets[s];
+    }
+  }
+}
+
+// token_meta from the slot table; slots past num_slots run base only.
+__device__ __forceinline__ TokenMeta token_meta_from(const GemvParams& p, const SlotTable& t, int g, int mt,
+                                                     int lane) {
+  TokenMeta m;
+  m.g = lane < mt && g >= 0 && g < p.num_slots ? g : -1;
+  const int gs = max(m.g, 0);
+  const int src = (gs & 63) << 2;
+  const int c = gs >> 6;
+  m.r = 0;
+  m.stride = 1;
+  m.scale = 0.f;
+  m.boff = 0;
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    if (64 * cc >= p.num_slots) break;  // uniform
+    const int r = __builtin_amdgcn_ds_bpermute(src, t.r[cc]);
+    const int st = __builtin_amdgcn_ds_bpermute(src, t.stride[cc]);
+    const float sc = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(t.scale[cc])));
+    const uint32_t blo = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(uint32_t(uint64_t(t.boff[cc])))));
+    const uint32_t bhi = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(uint32_t(uint64_t(t.boff[cc]) >> 32))));
+    if (c == cc) {
+      m.r = r;
+      m.stride = st;
+      m.scale = sc;
+      m.boff = int64_t((uint64_t(bhi) << 32) | blo);
+    }
+  }
+  if (m.g < 0 || m.r <= 0 || m.r > p.max_rank) {
     m.g = -1;
     m.r = 0;
     m.stride = 1;
@@ -558,7 +645,7 @@ __device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
   constexpr int kOut = kEntries / KZ > 0 ? kEntries / KZ : 1;
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + L::kMeta);
   uint16_t* zl = reinterpret_cast<uint16_t*>(lds + L::kZ);
-  for (int e = lane; e < TL::kXR * 192 / 8; e += 64) reinterpret_cast<uint4*>(zl)[e] = make_uint4(0, 0, 0, 0);
+  for (int e = lane; e < TL::kXR * L::kZRow / 8; e += 64) reinterpret_cast<uint4*>(zl)[e] = make_uint4(0, 0, 0, 0);
   const int total = tm->start[32];
   for (int o0 = 0; o0 < total; o0 += 64 * kOut) {
     const uint64_t* block = p.zp + int64_t(t0) * p.zw * KZ;
@@ -606,7 +693,7 @@ __device__ bool lora_gather_kz(const GemvParams& p, char* lds, int t0, int mt, u
       const int j = jv[q];
       const int ri = tm->r[i];
       const int s = int(j >= ri) + int(j >= 2 * ri) + int(j >= 3 * ri);  // slice of value j (3: past them)
-      if (need[q] && s < p.slices) zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(z));
+      if (need[q] && s < p.slices) zl[i * L::kZRow + s * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(z));
     }
     if (gave_up) return true;
   }
@@ -629,7 +716,7 @@ __device__ void lora_recompute(const GemvParams& p, char* lds, int t0, int mt, i
     const int ri = tm->r[i];
     if (tm->g[i] < 0 || j >= p.slices * ri) continue;
     const int s = j / ri;
-    zl[(i * 3 + s) * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(full_dot(p, t0 + i, tm->g[i], j)));
+    zl[i * L::kZRow + s * 64 + (j - s * ri)] = uint16_t(f32_to_bf16(full_dot(p, t0 + i, tm->g[i], j)));
   }
 }
 
@@ -720,6 +807,8 @@ inline int fill_lora_params(GemvParams& p, const GemvPlan& pl, const lf_lora* lo
   p.slice_offsets = lora->slice_offsets;
   p.slices = lora->num_slices;
   p.max_rank = lora->max_rank;
+  LF_REQUIRE(lora->num_slots >= 0, "num_slots must not be negative");
+  p.num_slots = lora->num_slots;
   p.zw = lora->num_slices * lora->max_rank;
   p.units = pl.units;
   p.kz = pl.kz;

@@ -105,4 +105,21 @@ __device__ __forceinline__ u32x4 global_load128_untracked_masked(const void* ptr
   return v;
 }
 
+// A pointer computed from uniform values, moved to scalar registers.
+template <class T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  return reinterpret_cast<const T*>((uint64_t(hi) << 32) | lo);
+}
+
+// An ordinary 16-byte load from global memory at a uniform base plus a
+// 32-bit per-lane byte offset (a global, not flat, load: flat loads also
+// count as LDS operations and hold back the next direct copy).
+__device__ __forceinline__ u32x4 global_load128(const void* base, uint32_t off) {
+  typedef const __attribute__((address_space(1))) char* GPtr;
+  return *(const __attribute__((address_space(1))) u32x4*)((GPtr)base + off);
+}
+
 }  // namespace lf

@@ -71,6 +71,7 @@ constexpr int kXSlot = kTokens * 128;  // one x block: 32 tokens x 64 bf16
 constexpr int kWGroup = kRows * 128;   // one weight group: 32 rows x 4 blocks x 32 packed bytes
 constexpr int kFirstSteps = 8;         // first-unit MFMA steps per base wave (8 x 8 covers a 2048-k slice)
 constexpr int kSlotsPerWave = kTokens / kBase;  // expand: the tile's distinct slots, one batch per wave
+constexpr int kContractAfter = 1;  // the loop block after which a producing wave contracts the first unit
 
 // Tile shape for the shared LoRA helpers (z staged for 32 tokens).
 struct WideTile {
@@ -78,33 +79,31 @@ struct WideTile {
   static constexpr int kRT = 2;
   static constexpr int kR = kRows;
   static constexpr int kTT = 1;
-  // Eight polled partials per lane and batch: sixteen need more registers
-  // than a ninth wave leaves (three waves on one SIMD, 168 VGPRs each).
+  // Sixteen polled partials per lane and batch: a tile's partials in one
+  // batch (the plan keeps 32 x zw x kz to 1024 where it can).
   static constexpr int kGatherEntries = 8;
+  // z rows 400 bytes apart: the 32 token rows of an MFMA operand read start
+  // on 16 different 4-bank groups (384 bytes apart, only two).
+  static constexpr int kZRow = 200;
 };
 using WL = LoraLds<WideTile>;
+
+// The launch parameters through a pointer the compiler cannot see through:
+// fields read after this are loaded (scalar loads from the kernarg segment)
+// where they are used, instead of being held in scalar registers from the
+// kernel's start across the weight loop.
+// (The kernels' only argument is the GemvParams, at offset 0 of the kernarg
+// segment.)
+__device__ __forceinline__ const GemvParams& reload() {
+  auto q = (const __attribute__((address_space(4))) GemvParams*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(q));
+  return *(const GemvParams*)q;
+}
 
 // Global row of local row r: a plain group's rows are contiguous; in
 // SwiGLU-output mode rows 0..15 are gate rows from lo, 16..31 the up rows
 // from hi.
 __device__ __forceinline__ int wrow(int lo, int hi, int r) { return r < 16 ? lo + r : hi + (r - 16); }
-
-// vmcnt(n) for a runtime n (used once per launch; anything above 31 waits
-// for everything, which is always safe).
-__device__ __forceinline__ void wait_vm_any(int n) {
-  switch (n) {
-#define LF_WAIT_CASE(c) \
-  case c: wait_vm<c>(); break;
-    LF_WAIT_CASE(1) LF_WAIT_CASE(2) LF_WAIT_CASE(3) LF_WAIT_CASE(4) LF_WAIT_CASE(5) LF_WAIT_CASE(6)
-    LF_WAIT_CASE(7) LF_WAIT_CASE(8) LF_WAIT_CASE(9) LF_WAIT_CASE(10) LF_WAIT_CASE(11) LF_WAIT_CASE(12)
-    LF_WAIT_CASE(13) LF_WAIT_CASE(14) LF_WAIT_CASE(15) LF_WAIT_CASE(16) LF_WAIT_CASE(17) LF_WAIT_CASE(18)
-    LF_WAIT_CASE(19) LF_WAIT_CASE(20) LF_WAIT_CASE(21) LF_WAIT_CASE(22) LF_WAIT_CASE(23) LF_WAIT_CASE(24)
-    LF_WAIT_CASE(25) LF_WAIT_CASE(26) LF_WAIT_CASE(27) LF_WAIT_CASE(28) LF_WAIT_CASE(29) LF_WAIT_CASE(30)
-    LF_WAIT_CASE(31)
-#undef LF_WAIT_CASE
-    default: wait_vm<0>(); break;
-  }
-}
 
 // The block scales of the group's 32 rows over blocks kb0 .. kb0 + nb - 1 into
 // the wave's scale area: row j at j * sc_stride floats (sc_stride a power of
@@ -159,45 +158,74 @@ struct WideB {
   uint4 bf[kSlotsPerWave];
 };
 
-__device__ __forceinline__ void expand_request(const GemvParams& p, const TileMeta* tm, WideB& b, int lo, int hi,
+// The tile's distinct slots that this wave expands (wave + kBase q, q <
+// kSlotsPerWave), in scalar registers: each lane reads one entry of the list
+// (one batch of LDS reads and one wait), and the wave's entries are taken by
+// lane reads, so the loops over slots, slices and rank groups branch on
+// scalars. Entries at or past nd are not used.
+struct WaveSlots {
+  int nd;
+  int g[kSlotsPerWave];
+  int r[kSlotsPerWave];
+  int stride[kSlotsPerWave];
+  int64_t boff[kSlotsPerWave];
+};
+
+__device__ __forceinline__ WaveSlots wave_slots(const TileMeta* tm, int wave, int lane) {
+  const int l = lane & 31;
+  const int vg = tm->dslot[l];
+  const int vr = tm->dr[l];
+  const int vst = tm->dstride[l];
+  const uint64_t vb = uint64_t(tm->dboff[l]);
+  const int vnd = tm->nd;
+  WaveSlots w;
+  w.nd = __builtin_amdgcn_readfirstlane(vnd);
+#pragma unroll
+  for (int q = 0; q < kSlotsPerWave; ++q) {
+    const int d = wave + kBase * q;
+    w.g[q] = __builtin_amdgcn_readlane(vg, d);
+    w.r[q] = __builtin_amdgcn_readlane(vr, d);
+    w.stride[q] = __builtin_amdgcn_readlane(vst, d);
+    w.boff[q] = int64_t((uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(vb >> 32)), d))) << 32) |
+                        uint32_t(__builtin_amdgcn_readlane(int(uint32_t(vb)), d)));
+  }
+  return w;
+}
+
+__device__ __forceinline__ void expand_request(const GemvParams& p, const WaveSlots& ws, WideB& b, int lo, int hi,
                                                int wave, int lane) {
-  const int nd = tm->nd;
   const int row = wrow(lo, hi, lane & 31);
   const int j0 = 8 * (lane >> 5);
 #pragma unroll
   for (int q = 0; q < kSlotsPerWave; ++q) {
-    const int d = wave + kBase * q;
-    const bool live = d < nd;
-    const int dd = live ? d : 0;
-    b.bf[q] = *reinterpret_cast<const uint4*>(b8_at(p, tm->dboff[dd], tm->dstride[dd], tm->dr[dd], row, j0, live).src);
+    const bool live = wave + kBase * q < ws.nd;
+    const int qq = live ? q : 0;
+    b.bf[q] = *reinterpret_cast<const uint4*>(b8_at(p, ws.boff[qq], ws.stride[qq], ws.r[qq], row, j0, live).src);
   }
 }
 
-__device__ __forceinline__ void expand_fix(const TileMeta* tm, WideB& b, int lo, int hi, int wave, int lane) {
-  const int nd = tm->nd;
+__device__ __forceinline__ void expand_fix(const WaveSlots& ws, WideB& b, int lo, int hi, int wave, int lane) {
   const int row = wrow(lo, hi, lane & 31);
   const int j0 = 8 * (lane >> 5);
 #pragma unroll
   for (int q = 0; q < kSlotsPerWave; ++q) {
-    const int d = wave + kBase * q;
-    if (d >= nd) break;  // uniform
-    const int st = tm->dstride[d];
-    const int cnt = min(8, tm->dr[d] - j0);
-    if (st >= 8) b.bf[q] = keep_first(b.bf[q], cnt);
-    else b.bf[q] = b8_fix(b.bf[q], B8{nullptr, int((tm->dboff[d] + int64_t(row) * st + j0) & 7), cnt});
+    if (wave + kBase * q >= ws.nd) break;
+    const int cnt = min(8, ws.r[q] - j0);
+    if (ws.stride[q] >= 8) b.bf[q] = keep_first(b.bf[q], cnt);
+    else b.bf[q] = b8_fix(b.bf[q], B8{nullptr, int((ws.boff[q] + int64_t(row) * ws.stride[q] + j0) & 7), cnt});
   }
 }
 
 // delta[token][row] = sum over this wave's slots g of z_g[token] . B_g[row] for
 // the tokens routed to g and the rows of the slice the z values belong to.
-__device__ __forceinline__ f32x16 expand_wide(const GemvParams& p, const char* lds, const WideB& b,
-                                              const int (&bounds)[4], int lo, int hi, int wave, int lane) {
+__device__ __forceinline__ f32x16 expand_wide(const GemvParams& p, const char* lds, const WaveSlots& ws,
+                                              const WideB& b, int lo, int hi, int wave, int lane) {
   const TileMeta* tm = reinterpret_cast<const TileMeta*>(lds + WL::kMeta);
+  const int bounds[3] = {0, __builtin_amdgcn_readfirstlane(tm->bounds[1]), __builtin_amdgcn_readfirstlane(tm->bounds[2])};
   const uint16_t* zl = reinterpret_cast<const uint16_t*>(lds + WL::kZ);
   f32x16 dacc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) dacc[e] = 0.f;
-  const int nd = tm->nd;
   const int i = lane & 31;  // token (A row) and local row (B column) of this lane
   const int g8 = 8 * (lane >> 5);
   const int row = wrow(lo, hi, i);
@@ -208,18 +236,14 @@ __device__ __forceinline__ f32x16 expand_wide(const GemvParams& p, const char* l
   const int gi = tm->g[i];
 #pragma unroll
   for (int q = 0; q < kSlotsPerWave; ++q) {
-    const int d = wave + kBase * q;
-    if (d >= nd) break;  // uniform
-    const int g = tm->dslot[d];
-    const int rk = tm->dr[d];
+    if (wave + kBase * q >= ws.nd) break;
     for (int s = s_lo; s <= s_hi; ++s) {
-      for (int h = 0; h < 4; ++h) {
-        if (16 * h >= rk) break;  // uniform
-        const uint4 zv = *reinterpret_cast<const uint4*>(zl + (i * 3 + s) * 64 + 16 * h + g8);
-        const uint4 zf = gi == g ? zv : make_uint4(0, 0, 0, 0);
+      for (int h = 0; 16 * h < ws.r[q]; ++h) {
+        const uint4 zv = *reinterpret_cast<const uint4*>(zl + i * WL::kZRow + s * 64 + 16 * h + g8);
+        const uint4 zf = gi == ws.g[q] ? zv : make_uint4(0, 0, 0, 0);
         uint4 bv = b.bf[q];
         if (h > 0) {
-          const B8 b8 = b8_at(p, tm->dboff[d], tm->dstride[d], rk, row, 16 * h + g8, true);
+          const B8 b8 = b8_at(p, ws.boff[q], ws.stride[q], ws.r[q], row, 16 * h + g8, true);
           bv = b8_fix(*reinterpret_cast<const uint4*>(b8.src), b8);
         }
         const uint4 bb = cs == s ? bv : make_uint4(0, 0, 0, 0);
@@ -230,21 +254,314 @@ __device__ __forceinline__ f32x16 expand_wide(const GemvParams& p, const char* l
   return dacc;
 }
 
+// A producing workgroup's first shrink unit, contracted on the VALU by the
+// base waves. The unit is cut into pieces of one A row x 512 k (1 KiB, one
+// load in which each 16-lane quarter reads 256 contiguous bytes). A pass
+// covers rp rows from j0 over c k-chunks (c = 1, 2, 4 or 8, the slice's
+// chunks rounded up to a power of two, at most 8; rp * c = 8 pw): wave w
+// takes chunk c ub + w % c of rows j0 + (w / c) pw .. + pw (pw <= R), with
+// the matching 1 KiB of x[t]. Lane l owns k = 512 chunk + 8 l; lanes past
+// the slice read x as zero (their A loads stay inside the row). The first
+// pass is requested before the x copies; further passes (more rows, slices
+// longer than 8 chunks) run after it.
+constexpr int kPieceK = 512;
+// Rows per wave and pass (pw): R = 4 for a unit contracted inside the weight
+// loop (fewer registers held across it), 8 otherwise.
+template <int R>
+struct UnitPieces {
+  u32x4 x;    // as loaded (lanes past the slice read k = 0; masked when used)
+  bool live;  // this lane's k is inside the slice
+  u32x4 a[R];
+};
+
+struct PassShape {
+  int c;   // k-chunks per pass
+  int rp;  // rows per pass
+  int pw;  // rows per wave
+};
+
+template <int R>
+__device__ __forceinline__ PassShape pass_shape(const Unit& un, int j0) {
+  const int chunks = (un.steps * 32 + kPieceK - 1) / kPieceK;
+  PassShape ps;
+  ps.c = chunks >= 8 ? 8 : chunks >= 4 ? (chunks == 4 ? 4 : 8) : chunks >= 2 ? (chunks == 2 ? 2 : 4) : 1;
+  const int step = 8 / ps.c;  // rp is a multiple of 8 / c
+  const int rest = (un.rows - j0 + step - 1) / step * step;
+  ps.rp = min(rest, R * 8 / ps.c);
+  ps.pw = ps.rp * ps.c / 8;
+  return ps;
+}
+
+// Ordinary (tracked) loads: the compiler waits for them before their first
+// use. Loads the compiler does not track must not be used here: the row
+// count is a runtime value, and a branch around such a load lets the
+// compiler copy its destination register before the data has arrived.
+template <int R>
+__device__ __forceinline__ void unit_pieces(const GemvParams& p, const Unit& un, int j0, int ub, const PassShape& ps,
+                                            int wave, int lane, UnitPieces<R>& f) {
+  const int len = un.steps * 32;
+  const int kofs = (ps.c * ub + wave % ps.c) * kPieceK + 8 * lane;
+  const bool live = kofs < len;
+  const uint32_t voff = uint32_t(live ? kofs : 0) * 2u;
+  // (No arithmetic on the loaded values here: it would make the compiler
+  // wait for them before the copies that follow.)
+  f.x = global_load128(uniform_ptr(p.x + int64_t(un.t) * p.x_stride + un.kb), voff);
+  f.live = live;
+  const int r0 = j0 + (wave / ps.c) * ps.pw;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    f.a[i] = u32x4{0u, 0u, 0u, 0u};
+    if (i < ps.pw) {  // uniform
+      const int row = min(r0 + i, un.rows - 1);
+      f.a[i] = global_load128(uniform_ptr(p.a_store + un.aoff + int64_t(row) * p.k + un.kb), voff);
+    }
+  }
+}
+
+// v[i] += sum over this lane's 8 k of x * A[row i] (fp32, in k order), i < pw.
+template <int R>
+__device__ __forceinline__ void unit_dots(const UnitPieces<R>& f, int pw, float (&v)[8]) {
+  const u32x4 x = f.live ? f.x : u32x4{0u, 0u, 0u, 0u};
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (i >= pw) continue;  // uniform
+    const uint32_t as[4] = {f.a[i].x, f.a[i].y, f.a[i].z, f.a[i].w};
+    float acc = v[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = __builtin_fmaf(bf16_lo(xs[e]), bf16_lo(as[e]), acc);
+      acc = __builtin_fmaf(bf16_hi(xs[e]), bf16_hi(as[e]), acc);
+    }
+    v[i] = acc;
+  }
+}
+
+// Sums v[0..7] over the wave's 64 lanes in 10 exchanges (each step halves
+// the values a lane keeps); lane l with l % 8 == 0 returns the sum of row
+// 4 (l / 32 % 2) + 2 (l / 16 % 2) + (l / 8 % 2).
+__device__ __forceinline__ float unit_reduce(float (&v)[8], int lane) {
+  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+  float h4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float keep = b5 ? v[i + 4] : v[i];
+    const float give = b5 ? v[i] : v[i + 4];
+    h4[i] = keep + __shfl_xor(give, 32, 64);
+  }
+  float h2[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float keep = b4 ? h4[i + 2] : h4[i];
+    const float give = b4 ? h4[i] : h4[i + 2];
+    h2[i] = keep + __shfl_xor(give, 16, 64);
+  }
+  float s = (b3 ? h2[1] : h2[0]) + __shfl_xor(b3 ? h2[0] : h2[1], 8, 64);
+  s += __shfl_xor(s, 4, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 1, 64);
+  return s;
+}
+
+// The base waves' part of a first unit that takes several passes (contracted
+// before the weight loop): every pass, then this wave's partial rows into red
+// (the pass's other rows as zero), then the wave counts in.
+__device__ void unit_contract(const GemvParams& p, const Unit& un, float* red, int* done, int wave, int lane) {
+  const int len = un.steps * 32;
+  const int rsel = 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
+  for (int j0 = 0; j0 < un.rows;) {
+    const PassShape ps = pass_shape<8>(un, j0);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    for (int ub = 0; ub == 0 || ub * ps.c * kPieceK < len; ++ub) {
+      UnitPieces<8> f;
+      unit_pieces(p, un, j0, ub, ps, wave, lane, f);
+      unit_dots(f, ps.pw, v);
+    }
+    const float s = unit_reduce(v, lane);
+    if (lane < ps.rp) red[wave * 192 + j0 + lane] = 0.f;
+    if ((lane & 7) == 0 && rsel < ps.pw) red[wave * 192 + j0 + (wave / ps.c) * ps.pw + rsel] = s;
+    j0 += ps.rp;
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the partial rows are in LDS
+  if (lane == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// A unit whose rows fit one pass and whose slice fits one group of c chunks
+// is contracted from the first pass alone (inside the weight loop).
+__device__ __forceinline__ bool unit_single_pass(const Unit& un, const PassShape& ps) {
+  return un.rows <= ps.rp && un.steps * 32 <= ps.c * kPieceK;
+}
+
+__device__ __forceinline__ void unit_contract_single(const UnitPieces<4>& pre, const PassShape& ps, float* red,
+                                                     int* done, int wave, int lane) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  unit_dots(pre, ps.pw, v);
+  const float s = unit_reduce(v, lane);
+  const int rsel = 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
+  if (lane < ps.rp) red[wave * 192 + lane] = 0.f;
+  if ((lane & 7) == 0 && rsel < ps.pw) red[wave * 192 + (wave / ps.c) * ps.pw + rsel] = s;
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the partial rows are in LDS
+  if (lane == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Tile metadata of the wide kernel (the fields its base waves and the
+// recompute read): per token g, r and scale; the distinct live slots in
+// order of first use with their rank, B stride and B offset; the slice
+// bounds; then the ready flag. One ballot per distinct slot records the
+// slot's first token in a register lane; the slot fields come from that
+// token's lane by shuffles after the loop (no LDS stores inside it).
+__device__ void lora_meta_wide(char* lds, const TokenMeta& m, int sbound, int lane) {
+  TileMeta* tm = reinterpret_cast<TileMeta*>(lds + WL::kMeta);
+  if (lane < 32) {
+    tm->g[lane] = m.g;
+    tm->r[lane] = m.r;
+    tm->scale[lane] = m.scale;
+  }
+  if (lane < 4) tm->bounds[lane] = sbound;
+  uint64_t left = __ballot(m.g >= 0);  // (lanes past the tile hold g = -1)
+  int nd = 0;
+  int first = 0;  // lane d < nd: the first token of distinct slot d
+  while (left) {
+    const int f = __builtin_ctzll(left);
+    const int gf = __builtin_amdgcn_readlane(m.g, f);
+    first = lane == nd ? f : first;
+    left &= ~__ballot(m.g == gf);
+    ++nd;
+  }
+  const int src = first << 2;
+  const int dg = __builtin_amdgcn_ds_bpermute(src, m.g);
+  const int dr = __builtin_amdgcn_ds_bpermute(src, m.r);
+  const int dst = __builtin_amdgcn_ds_bpermute(src, m.stride);
+  const uint32_t blo = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(uint32_t(uint64_t(m.boff)))));
+  const uint32_t bhi = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(uint32_t(uint64_t(m.boff) >> 32))));
+  if (lane < nd) {
+    tm->dslot[lane] = dg;
+    tm->dr[lane] = dr;
+    tm->dstride[lane] = dst;
+    tm->dboff[lane] = int64_t((uint64_t(bhi) << 32) | blo);
+  }
+  if (lane == 0) tm->nd = nd;
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the metadata is in LDS
+  if (lane == 0) *(volatile __attribute__((address_space(3))) int*)(&tm->ready) = 1;
+}
+
+// z of the tile into LDS, fixed layout. Lane-group q (one per lane and
+// batch) owns vg = 8 / KZ consecutive values of one token and slice: token
+// i = q / gt, slice s = (q % gt) / gs, positions j0 = vg (q % gs) .. + vg,
+// where gs = pl / vg groups cover the part of a slice the expand reads (pl:
+// max_rank rounded up to 16) and gt = slices * gs. A lane polls its vg x KZ
+// tagged partials until every one it needs carries the call's tag, sums the
+// k-slices in registers and writes its values as bf16 with one store (zero
+// past the token's rank, for base-only tokens and tokens past the batch).
+// Token i's rank comes from lane i of the token metadata by a shuffle; no
+// list is searched. Returns true when a wait gave up (the caller recomputes).
+template <int KZ>
+__device__ bool gather_wide_kz(const GemvParams& p, char* lds, const TokenMeta& m, int t0, uint32_t tag, int lane) {
+  constexpr int VG = 8 / KZ;
+  char* zl = lds + WL::kZ;
+  const int pl = (p.max_rank + 15) & ~15;
+  const int gs = pl / VG;
+  const int gt = p.slices * gs;
+  const int total = kTokens * gt;
+  const uint64_t* block = p.zp + int64_t(t0) * p.zw * KZ;
+  bool gave_up = false;
+  for (int q0 = 0; q0 < total; q0 += 64) {
+    const int q = q0 + lane;
+    const int i = min(q / gt, kTokens - 1);
+    const int rem = q - i * gt;
+    const int s = rem / gs;
+    const int j0 = (rem - s * gs) * VG;
+    const int ri = __builtin_amdgcn_ds_bpermute(i << 2, m.r);
+    const int cnt = q < total ? max(0, min(VG, ri - j0)) : 0;
+    const int64_t base = (int64_t(i) * p.zw + s * ri + j0) * KZ;
+    uint64_t v[VG][KZ];
+    for (int spins = 0;; ++spins) {
+#pragma unroll
+      for (int vv = 0; vv < VG; ++vv)
+#pragma unroll
+        for (int ks = 0; ks < KZ; ++ks)  // unconditional: no per-load branch
+          v[vv][ks] = tagged_load(block + (vv < cnt ? base + vv * KZ + ks : 0));
+      bool ok = true;
+#pragma unroll
+      for (int vv = 0; vv < VG; ++vv)
+#pragma unroll
+        for (int ks = 0; ks < KZ; ++ks) ok = ok && (vv >= cnt || uint32_t(v[vv][ks] >> 32) == tag);
+      if (__all(ok)) break;
+      if (spins > p.spin_limit) {
+        gave_up = true;  // (cannot happen while producers run: they wait for nothing)
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    uint32_t w[(VG + 1) / 2];
+#pragma unroll
+    for (int h = 0; h < (VG + 1) / 2; ++h) {
+      float z2[2] = {0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int vv = 2 * h + e;
+        if (vv >= VG) break;
+        float z = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KZ; ++ks) z += __uint_as_float(uint32_t(v[vv][ks]));
+        z2[e] = vv < cnt ? z : 0.f;
+      }
+      w[h] = pack_bf16x2(z2[0], z2[1]);
+    }
+    if (q < total) {
+      char* dst = zl + (i * WL::kZRow + s * 64 + j0) * 2;
+      if constexpr (VG == 8) *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+      else if constexpr (VG == 4) *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+      else if constexpr (VG == 2) *reinterpret_cast<uint32_t*>(dst) = w[0];
+      else *reinterpret_cast<uint16_t*>(dst) = uint16_t(w[0]);
+    }
+  }
+  return gave_up;
+}
+
+__device__ void gather_wide(const GemvParams& p, char* lds, const TokenMeta& m, int t0, int mt, uint32_t tag,
+                            int lane) {
+  bool gave_up;
+  switch (p.kz) {
+    case 1: gave_up = gather_wide_kz<1>(p, lds, m, t0, tag, lane); break;
+    case 2: gave_up = gather_wide_kz<2>(p, lds, m, t0, tag, lane); break;
+    case 4: gave_up = gather_wide_kz<4>(p, lds, m, t0, tag, lane); break;
+    default: gave_up = gather_wide_kz<8>(p, lds, m, t0, tag, lane); break;
+  }
+  if (gave_up) {
+    // Every z value is recomputed from x and A (the status word reports it);
+    // the area is cleared first, as batches after the one that gave up were
+    // not written.
+    uint4* z4 = reinterpret_cast<uint4*>(lds + WL::kZ);
+    for (int e = lane; e < kTokens * WL::kZRow / 8; e += 64) z4[e] = make_uint4(0, 0, 0, 0);
+    lora_recompute<WideTile>(p, lds, t0, mt, lane);
+  }
+}
+
 // The LoRA wave of a wide workgroup: publishes the workgroup's first shrink
 // unit as soon as the base waves have counted in, builds the tile metadata,
 // produces the other units (small grids only), gathers z, and takes its part
 // in the workgroup's two remaining barriers (z ready; partial tiles in LDS)
 // before it counts the workgroup out of the call.
 __device__ __forceinline__ void lora_wave(const GemvParams& p, char* lora_lds, float* red, int* prod_done, int g_tile,
-                                       uint32_t epoch, int t0, int mt, int lane) {
-  const TokenMeta tmeta = token_meta(p, g_tile, mt, lane);
+                                       int sbound, const SlotTable& stab, uint32_t epoch, int t0, int mt, int lane) {
+  // Issue priority over the two base waves that share this wave's SIMD: the
+  // chain below is short but serial, and at equal priority it gets about a
+  // third of the SIMD's issue slots while the base waves stream.
+  __builtin_amdgcn_s_setprio(3);
+  const TokenMeta tmeta =
+      slot_table_usable(p) ? token_meta_from(p, stab, g_tile, mt, lane) : token_meta(p, g_tile, mt, lane);
   Unit un0{};
   const bool has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
   const uint32_t tag = __builtin_amdgcn_readfirstlane(epoch) + 1u;
+  lora_meta_wide(lora_lds, tmeta, sbound, lane);  // first: the base waves request B with it before their loop
   if (has0) publish_first_unit<kBase>(p, red, prod_done, un0, tag, lane);
-  lora_meta<WideTile>(lora_lds, tmeta, p.slices, lane);
   produce_other_units<kFirstSteps>(p, tag, lane);
-  lora_gather<WideTile>(p, lora_lds, t0, mt, tag, lane);
+  gather_wide(p, lora_lds, tmeta, t0, mt, tag, lane);
   const uint32_t departed = depart_issue(p.ce, lane);  // after the last partial load
   lds_barrier();  // z and the tile metadata are in LDS
   lds_barrier();  // the partial tiles are in LDS
@@ -262,7 +579,8 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   __shared__ float table[16];
   __shared__ __attribute__((aligned(16))) uint32_t pt[kExact ? 4 : 256 * kCP];
   __shared__ __attribute__((aligned(16))) char lora_lds[kLora ? WL::kBytes : 16];
-  __shared__ int prod_done;  // base waves that have written their first-unit partials
+  __shared__ int prod_done;   // base waves that have written their first-unit partials
+  __shared__ int table_done;  // (LoRA) base waves 0..3 that have written their part of the decode table
   extern __shared__ __attribute__((aligned(16))) char scale_lds[];  // kBase * p.sc_bytes (+16)
 
   const int xcc = blockIdx.x & 7;
@@ -326,78 +644,135 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
 
   // Codebook (and the LoRA slice bounds) through scalar loads: no vector
   // load waits behind the copies.
+  // (With LoRA: base waves only, once their copies are out, so the LoRA
+  // wave's early barrier does not wait for these loads and the values are
+  // not held across the copy issue.)
   float cb[16];
+  auto load_codebook = [&]() {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) cb[i] = sload(p.code, i);
-  int bounds[4] = {0, 0, 0, 0};
-  if constexpr (kLora) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) bounds[q] = q <= p.slices ? sload(p.slice_offsets, q) : 0;
-  }
+    for (int i = 0; i < 16; ++i) cb[i] = sload(p.code, i);
+  };
+  if constexpr (!kLora) load_codebook();
 
-  // A producing workgroup's first shrink unit: its fragments are requested
-  // ahead of the weight copies (untracked loads), so they are not queued
-  // behind the weight stream; the base waves contract them once they land.
-  Unit un0{};
-  bool has0 = false;
-  FirstFragsN<kFirstSteps> pre;
+  // With LoRA, the LoRA wave clears the workgroup's flags and requests the
+  // call epoch, its tile's token slots and the per-slot metadata before one
+  // early barrier, so those loads are ahead of every copy of the workgroup; after
+  // it the base waves build the decode table behind their copies and count
+  // in on table_done, and the LoRA wave meets them again only at the z
+  // barrier (a barrier after the copies would hold it until the base waves
+  // had issued all of theirs).
   uint32_t epoch = 0;
   int g_tile = -1;
-  int after_unit = 0;  // copies issued after the unit's fragments
-  if (base) {
-    if constexpr (kLora) {
-      has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
-      if (has0) first_frags<kFirstSteps, kBase>(p, un0, wave, lane, pre);
+  int g0 = -1;  // slot of the token of this workgroup's first unit (base waves)
+  int sbound = 0;  // (LoRA wave) slice_offsets[min(lane % 4, slices)]
+  SlotTable stab;
+  if constexpr (kLora) {
+    if (base) {
+      g0 = sload(p.token_slots, unit_token(p, min(int(blockIdx.x), p.units - 1)));
+      barrier_only();  // (no wait: the base waves' scalar loads stay in flight)
+    } else {
+      if (lane == 0) {
+        reinterpret_cast<TileMeta*>(lora_lds + WL::kMeta)->ready = 0;
+        prod_done = 0;
+        table_done = 0;
+      }
+      epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      g_tile = p.token_slots[t0 + min(lane, mt - 1)];
+      sbound = p.slice_offsets[min(lane & 3, p.slices)];
+      if (slot_table_usable(p)) slot_table_load(p, lane, stab);
+      lds_barrier();  // the flags are cleared
     }
-    if (nb > 0) {
-      after_unit += issue_scales(p, mysc, lo, hi, kb0, nb, lane);
-#pragma unroll
-      for (int g2 = 0; g2 < kDWG; ++g2)
-        if (g2 < groups) {
-          issue_w(g2, g2);
-          after_unit += 4;
-        }
-#pragma unroll
-      for (int s = 0; s < kDX; ++s)
-        if (s < nb) {
-          issue_x(s, s);
-          after_unit += 4;
-        }
-    }
-  } else if constexpr (kLora) {
-    // The LoRA wave: the call epoch and the tile's token slots (vector loads;
-    // the barriers below wait for scalar loads and LDS only).
-    epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    g_tile = p.token_slots[t0 + min(lane, mt - 1)];
   }
 
-  if (threadIdx.x == 0) {
+  // Copies: the block scales, the first weight groups and the first x
+  // blocks, then (a producing workgroup) the first unit's A and x pieces.
+  // The base waves contract the pieces once they land (ordinary loads: the
+  // compiler waits for them, and as loads complete in issue order, for every
+  // copy before them; the x blocks are therefore requested first).
+  Unit un0{};
+  bool has0 = false;
+  bool single = false;  // the first unit is contracted inside the loop (from pre4)
+  UnitPieces<4> pre4;
+  if (base) {
+    if (nb > 0) {
+      issue_scales(p, mysc, lo, hi, kb0, nb, lane);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) table[i] = cb[i];
+      for (int g2 = 0; g2 < kDWG; ++g2)
+        if (g2 < groups) issue_w(g2, g2);
+    }
+    if (nb > 0) {
+#pragma unroll
+      for (int s = 0; s < kDX; ++s)
+        if (s < nb) issue_x(s, s);
+    }
     if constexpr (kLora) {
-      reinterpret_cast<TileMeta*>(lora_lds + WL::kMeta)->ready = 0;
-      prod_done = 0;
+      has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of_slot(p, blockIdx.x, g0, un0);
+      if (has0) {
+        single = unit_single_pass(un0, pass_shape<4>(un0, 0));
+        if (single) unit_pieces(p, un0, 0, 0, pass_shape<4>(un0, 0), wave, lane, pre4);
+      }
     }
   }
-  if constexpr (!kExact) {
-    lds_barrier();
-    if (threadIdx.x < 256) {
-      const uint32_t v = pack_bf16x2(table[threadIdx.x >> 4], table[threadIdx.x & 15]);
-      uint4* dst = reinterpret_cast<uint4*>(pt + threadIdx.x * kCP);
+
+  if constexpr (kLora) {
+    // Waves 0..3: entry t = threadIdx.x of the pair table (and the codebook
+    // for the exact decode), from the codebook in scalar registers.
+    if (base && wave < 4) {
+      load_codebook();
+      const int t = threadIdx.x;
+      float c_lo = cb[0], c_hi = cb[0];
 #pragma unroll
-      for (int c = 0; c < kCP / 4; ++c) dst[c] = make_uint4(v, v, v, v);
+      for (int q = 1; q < 16; ++q) {
+        c_lo = (t >> 4) == q ? cb[q] : c_lo;
+        c_hi = (t & 15) == q ? cb[q] : c_hi;
+      }
+      if (t < 16) table[t] = c_hi;
+      if constexpr (!kExact) {
+        const uint32_t v = pack_bf16x2(c_lo, c_hi);
+        uint4* dst = reinterpret_cast<uint4*>(pt + t * kCP);
+#pragma unroll
+        for (int c = 0; c < kCP / 4; ++c) dst[c] = make_uint4(v, v, v, v);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's entries are in LDS
+      if (lane == 0) __hip_atomic_fetch_add(&table_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+  } else {
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) table[i] = cb[i];
+    }
+    if constexpr (!kExact) {
+      lds_barrier();
+      if (threadIdx.x < 256) {
+        const uint32_t v = pack_bf16x2(table[threadIdx.x >> 4], table[threadIdx.x & 15]);
+        uint4* dst = reinterpret_cast<uint4*>(pt + threadIdx.x * kCP);
+#pragma unroll
+        for (int c = 0; c < kCP / 4; ++c) dst[c] = make_uint4(v, v, v, v);
+      }
+    }
+    lds_barrier();
   }
-  lds_barrier();
   const uint32_t* ptl = pt + (lane % kCP);
 
   // The base waves; the LoRA wave's code follows theirs (so nothing of the
   // streaming state is live across it).
   if (base) {
   if constexpr (kLora) {
+    while (*(const volatile __attribute__((address_space(3))) int*)(&table_done) < 4) __builtin_amdgcn_s_sleep(1);
+  }
+  // A producing wave contracts its part of a single-pass first unit inside
+  // the loop, after block kContractAfter: the pieces were requested before
+  // the refills of the blocks before it and have landed, and the loop is not
+  // held back until they do (a wave with fewer blocks contracts after the
+  // loop). Longer units are contracted here, before the loop, so their
+  // partials are not late for the other workgroups.
+  bool contract = false;
+  PassShape ps0{};
+  if constexpr (kLora) {
     if (has0) {
-      wait_vm_any(after_unit);  // the unit's fragments have landed (loads complete in order)
-      first_unit_partials<kFirstSteps, kBase>(p, un0, pre, red, &prod_done, wave, lane);
+      ps0 = pass_shape<4>(un0, 0);
+      if (single) contract = true;
+      else unit_contract(p, un0, red, &prod_done, wave, lane);
     }
   }
 
@@ -461,9 +836,19 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[e] = __builtin_fmaf(sc, d[e], acc[e]);
       }
+      if constexpr (kLora) {
+        if (bl == kContractAfter && contract) {
+          unit_contract_single(pre4, ps0, red, &prod_done, wave, lane);
+          contract = false;
+        }
+      }
     }
   }
+  if constexpr (kLora) {
+    if (contract) unit_contract_single(pre4, ps0, red, &prod_done, wave, lane);
+  }
   wait_vm<0>();
+  const GemvParams& pe = reload();  // the epilogue's parameters, read where used
 
   // With LoRA: the base waves request the B fragments of their slots once the
   // tile metadata is ready, the LoRA wave has gathered z, and after the
@@ -475,10 +860,11 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
     const TileMeta* tm = reinterpret_cast<const TileMeta*>(lora_lds + WL::kMeta);
     WideB eb;
     while (*(const volatile __attribute__((address_space(3))) int*)(&tm->ready) == 0) __builtin_amdgcn_s_sleep(1);
-    expand_request(p, tm, eb, lo, hi, wave, lane);
-    expand_fix(tm, eb, lo, hi, wave, lane);
+    const WaveSlots ws = wave_slots(tm, wave, lane);
+    expand_request(pe, ws, eb, lo, hi, wave, lane);
+    expand_fix(ws, eb, lo, hi, wave, lane);
     lds_barrier();  // z and the tile metadata are in LDS
-    dacc = expand_wide(p, lora_lds, eb, bounds, lo, hi, wave, lane);
+    dacc = expand_wide(pe, lora_lds, ws, eb, lo, hi, wave, lane);
   }
 
   // Sum the partial tiles: base wave w writes its accumulators (and delta
@@ -517,18 +903,18 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
       }
       const int row = wrow(lo, hi, col);
       float v = round_bf16(sum);
-      if (p.bias) v = round_bf16(v + bf16_to_f32(p.bias[row]));
+      if (pe.bias) v = round_bf16(v + bf16_to_f32(pe.bias[row]));
       if (routed) v += round_bf16(dsum * lscale);
       out[h] = round_bf16(v);
-      if (!p.gated_half && tok < mt) p.y[int64_t(t0 + tok) * p.y_stride + row] = uint16_t(f32_to_bf16(v));
+      if (!pe.gated_half && tok < mt) pe.y[int64_t(t0 + tok) * pe.y_stride + row] = uint16_t(f32_to_bf16(v));
     }
     // SwiGLU output h = bf16(bf16(silu(gate)) * up) for feature lo + jj (the
     // reference's activation after both LoRA adds, benchmarks/qwen35_decode_silu.py:60-61).
-    if (p.gated_half && tok < mt)
-      p.y[int64_t(t0 + tok) * p.y_stride + lo + jj] = uint16_t(f32_to_bf16(silu_times(out[0], out[1])));
+    if (pe.gated_half && tok < mt)
+      pe.y[int64_t(t0 + tok) * pe.y_stride + lo + jj] = uint16_t(f32_to_bf16(silu_times(out[0], out[1])));
   }
   } else {
-    if constexpr (kLora) lora_wave(p, lora_lds, red, &prod_done, g_tile, epoch, t0, mt, lane);
+    if constexpr (kLora) lora_wave(reload(), lora_lds, red, &prod_done, g_tile, sbound, stab, epoch, t0, mt, lane);
   }
 }
 
@@ -576,6 +962,33 @@ int64_t scale_area_bytes(int64_t nblk) { return (kRows * scale_stride(nblk) * 4 
 
 int device_cus();
 
+// Shrink units of the wide kernel: k-slices only as many as keep a tile's
+// partials (32 tokens x zw x kz) to one gather batch of 512 entries (8 per
+// lane of the LoRA wave) and leave a producer per unit, then 4-row ranges
+// (the VALU contraction takes any number of rows) until every workgroup up
+// to min(grid, CUs) produces one unit: no workgroup contracts a larger share
+// of the adapters' A than the others and holds the call's end.
+GemvPlan wide_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
+  GemvPlan pl;
+  pl.rows = kRows;
+  pl.row_groups = int(n / kRows);
+  pl.grid = pl.row_groups * int((m + kTokens - 1) / kTokens);
+  const int64_t cap = std::min<int64_t>(pl.grid, cus);
+  const int64_t nblk = k / 64;
+  int64_t kz = std::max<int64_t>(
+      1, std::min<int64_t>({nblk, 8, 512 / (int64_t(kTokens) * zw), cap / std::max<int64_t>(1, m)}));
+  while (kz & (kz - 1)) kz &= kz - 1;  // a power of two (the consumer sums the slices unrolled)
+  pl.kz = int(kz);
+  pl.kz_len = int((nblk + kz - 1) / kz) * 64;
+  const int64_t groups = (zw + 3) / 4;  // 4-row groups per token
+  const int64_t split = std::max<int64_t>(1, std::min<int64_t>(groups, cap / (m * kz)));
+  pl.urows = int((groups + split - 1) / split) * 4;
+  pl.usplit = int((groups * 4 + pl.urows - 1) / pl.urows);
+  pl.units = int(m) * pl.usplit * pl.kz;
+  pl.producers = int(cap);
+  return pl;
+}
+
 // Whether the wide decode kernel takes this call: more than 32 tokens, a K
 // whose rings and scale areas fit LDS (the smallest variant), and with LoRA
 // row groups that fill whole XCD octets (N a multiple of 256), shrink
@@ -590,7 +1003,7 @@ bool decode_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora) {
   if (smallest + kBase * area + 16 > kLdsBytes) return false;
   if (!lora) return true;
   if (n % (8 * kRows)) return false;
-  const GemvPlan pl = gemv_plan(m, n, k, device_cus(), lora->num_slices * lora->max_rank);
+  const GemvPlan pl = wide_plan(m, n, k, device_cus(), lora->num_slices * lora->max_rank);
   return pl.units <= 1024 && kPartialsOffset + m * pl.kz * lora->num_slices * lora->max_rank * 8 <= kWorkspaceHeader;
 }
 
@@ -618,7 +1031,7 @@ int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_
   p.sc_stride = int(scale_stride(nblk));
   p.sc_bytes = int(scale_area_bytes(nblk));
   if (lora) {
-    const GemvPlan pl = gemv_plan(m, w->n, w->k, device_cus(), lora->num_slices * lora->max_rank);
+    const GemvPlan pl = wide_plan(m, w->n, w->k, device_cus(), lora->num_slices * lora->max_rank);
     const int rc = fill_lora_params(p, pl, lora, m, workspace, workspace_bytes, withhold);
     if (rc != kOk) return rc;
   }

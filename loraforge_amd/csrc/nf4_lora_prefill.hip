@@ -58,6 +58,7 @@ struct PrefillParams {
   const int32_t* token_slots;
   const int32_t* slice_offsets;
   int slices;
+  int num_slots;      // entries of the per-slot arrays (0: not given; slots at or past it run base only)
   uint16_t* zpad;     // [m][slices * 64]
   int y_vec;          // 2: 16-byte aligned y rows, 1: 8-byte aligned, 0: neither
   uint32_t* zflags;   // [mtiles * zparts]: the call's tag once a producer's z rows are stored
@@ -80,6 +81,7 @@ constexpr int kMaxList = kBM;  // a tile routes to at most one slot per token
 __device__ void live_slots(const PrefillParams& p, int t0, int count, int* tslot, int* list) {
   for (int t = threadIdx.x; t < kThreads; t += blockDim.x) {
     int g = t < count ? p.token_slots[t0 + t] : -1;
+    if (p.num_slots > 0 && g >= p.num_slots) g = -1;
     const int r = g >= 0 ? p.ranks[g] : 0;
     if (r <= 0 || r > kZSlice) g = -1;  // rank 0 / contract violation: base only
     tslot[t] = g;
@@ -1018,6 +1020,8 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
     p.lscales = lora->scales;
     p.token_slots = lora->token_slots;
     p.slice_offsets = lora->slice_offsets;
+    LF_REQUIRE(lora->num_slots >= 0, "num_slots must not be negative");
+    p.num_slots = lora->num_slots;
     p.zflags = reinterpret_cast<uint32_t*>(ws + kWorkspaceHeader);  // after the decode header
     p.zpad = reinterpret_cast<uint16_t*>(ws + kWorkspaceHeader + kFlagRegion);
     p.ce = call_epoch_of(ws);

@@ -255,6 +255,7 @@ def _lora_struct(lora: LoraBatch, m: int, k: int, n: int, device):
     s.slice_offsets = lora.slice_offsets.data_ptr()
     s.num_slices = lora.num_slices
     s.max_rank = lora.max_rank
+    s.num_slots = g
     return s
 
 

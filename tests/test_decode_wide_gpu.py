@@ -106,3 +106,37 @@ def test_wide_matches_across_token_tiles(device):
     small = nf4_lora_linear(x[:64].contiguous(), q, st)
     torch.cuda.synchronize()
     assert torch.equal(big[:64], small)
+
+
+@pytest.mark.parametrize("slots", [1, 65, 256, 300])
+def test_wide_lora_slot_counts(slots, device):
+    """The LoRA wave loads the per-slot arrays whole (lane l: slots l, l + 64,
+    ...) when the pool has at most 256 slots and looks each token up by lane
+    shuffle; above that it reads each token's slot entries. Both against the
+    oracle, with tokens spread over the whole pool."""
+    m, n, k = 64, 1024, 2048
+    rng = np.random.default_rng(slots)
+    ranks = tuple(int(r) for r in rng.choice([4, 8, 16], slots))
+    token_slots = rng.integers(0, slots, m).astype(np.int32)
+    token_slots[:4] = [slots - 1, 0, -1, slots // 2]
+    case = _cases.fused_case(m, n, k, ranks=ranks, seed=slots, token_slots=token_slots)
+    x, q, st, lora, _ = to_device(case, device)
+    print(f"[wide-lora] slots={slots}", flush=True)
+    y = nf4_lora_linear(x, q, st, lora=lora)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+
+
+def test_wide_lora_slots_past_the_pool_run_base_only(device):
+    """With the pool's slot count given (it always is through nf4_lora_linear),
+    a token slot at or past it runs the base linear alone in the wide kernel."""
+    m, n, k = 48, 512, 1024
+    slots = 8
+    token_slots = np.arange(m, dtype=np.int32) % (slots + 4)  # 8..11 are past the pool
+    case = _cases.fused_case(m, n, k, ranks=(16,) * slots, seed=12, token_slots=token_slots)
+    x, q, st, lora, _ = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, lora=lora)
+    expect_case = dict(case)
+    expect_case["lora"] = dict(case["lora"], token_slots=np.where(token_slots >= slots, -1, token_slots).astype(np.int32))
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(expect_case))
