@@ -61,7 +61,14 @@ LAYERS = 64
 ROUNDS = 3
 
 TRAFFIC_FILE = ROOT / "profiles" / "decode_hbm_traffic.json"
-DECODE_SOURCE = ROOT / "loraforge_amd" / "csrc" / "nf4_gemv.hip"
+# The kernel that runs a decode batch: 1..32 tokens the narrow decode kernel,
+# 33..64 the wide one (32 rows x 32 tokens per workgroup).
+NARROW_SOURCE = ROOT / "loraforge_amd" / "csrc" / "nf4_gemv.hip"
+WIDE_SOURCE = ROOT / "loraforge_amd" / "csrc" / "nf4_decode_wide.hip"
+
+
+def decode_kernel(batch: int) -> tuple[str, Path]:
+    return ("nf4_decode_wide_kernel", WIDE_SOURCE) if batch > 32 else ("nf4_gemv_kernel", NARROW_SOURCE)
 
 
 def source_digest(path: Path) -> str:
@@ -80,7 +87,7 @@ def measured_traffic(batch: int):
         rec = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
         return None
-    if int(rec.get("batch", -1)) != batch or rec.get("source_sha256_16") != source_digest(DECODE_SOURCE):
+    if int(rec.get("batch", -1)) != batch or rec.get("source_sha256_16") != source_digest(decode_kernel(batch)[1]):
         return None
     return int(rec["traffic_bytes_per_launch"])
 
@@ -655,7 +662,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(head["frac"], 4),
             "traffic": measured_traffic(args.batch),
-            "kernel": "nf4_gemv_kernel",
+            "kernel": decode_kernel(args.batch)[0],
             "bytes_per_launch": head["bytes_per_call"],
             "us_per_launch": round(head["us_per_call"], 3),
             "timing": "HIP events on the graph-replay stream over the timed calls (includes the graph's "
@@ -728,4 +735,8 @@ if __name__ == "__main__":
             torch.cuda.synchronize()
     except Exception:  # noqa: BLE001 - best effort before exiting
         pass
+    # Under a profiler (rocprofv3 preloads its tool library and writes its
+    # results from exit hooks) the process ends normally.
+    if any(k.startswith("ROCPROF") for k in os.environ) or "rocprofiler" in os.environ.get("LD_PRELOAD", ""):
+        sys.exit(rc)
     os._exit(rc)
