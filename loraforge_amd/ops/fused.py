@@ -293,8 +293,8 @@ def nf4_lora_linear(
     ``swiglu=True``: the weight is a merged gate/up projection (gate rows
     ``0 .. N/2``, up rows ``N/2 .. N``; with LoRA, slices ``[0, N/2, N]``) and
     the result is ``h = bf16(bf16(silu(gate)) * up)``, ``[..., N/2]``, of the
-    LoRA-updated bf16 gate and up outputs. Batches of up to 32 tokens compute
-    it in the decode kernel's epilogue (no gate/up round trip, no second
+    LoRA-updated bf16 gate and up outputs. Batches of up to 64 tokens compute
+    it in the decode kernels' epilogue (no gate/up round trip, no second
     launch); larger ones run the linear and then ``silu_mul``.
 
     Above 64 tokens the library picks the prefill GEMM or the decode kernel
@@ -336,11 +336,9 @@ def nf4_lora_linear(
         if lora is not None and lora.num_slices != 2:
             raise ValueError("SwiGLU output with LoRA needs the two gate/up slices")
         width = n // 2
-        # Batches above 32 tokens run the linear and then the activation: their
-        # decode groups (32 rows, two token tiles) would take both gate/up
-        # slices' expand per workgroup, measured slower than the second launch
-        # (c3 at B = 64: 136 us fused against 134 us).
-        if m > 32:
+        # Batches above 64 tokens run the linear and then the activation (the
+        # activation is fused into the decode kernels' epilogue only).
+        if m > 64:
             from .activation import silu_mul
 
             if out is not None:
