@@ -571,8 +571,11 @@ __device__ __forceinline__ void lora_wave(const GemvParams& p, char* lora_lds, f
 // kDWG: weight group slots per wave (2, or 1 when a long K needs the LDS).
 // kLora: a ninth wave and the LoRA stages (row groups must fill whole XCD
 // octets, so every workgroup of the grid is a real one and counts in once).
-template <bool kExact, int kDWG, bool kLora>
+// kResidual (with kLora): no weight; y is the base and is updated in place
+// with each routed token's LoRA delta (the one-launch shrink + expand).
+template <bool kExact, int kDWG, bool kLora, bool kResidual = false>
 __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_wide_kernel(GemvParams p) {
+  static_assert(!kResidual || (kLora && !kExact), "the residual form is a LoRA-only variant");
   constexpr int kCP = kLora ? 8 : 16;  // pair-table copies (lane l reads copy l % kCP); 8 leave LDS for LoRA
   __shared__ __attribute__((aligned(16))) char wring[kBase * kDWG * kWGroup];
   __shared__ __attribute__((aligned(16))) char xring[kBase * kDX * kXSlot];
@@ -596,8 +599,8 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   const int lane = threadIdx.x & 63;
   const bool base = wave < kBase;
   const int nblk = p.k >> 6;
-  const int kb0 = base ? nblk * wave / kBase : 0;
-  const int nb = base ? nblk * (wave + 1) / kBase - kb0 : 0;
+  const int kb0 = base && !kResidual ? nblk * wave / kBase : 0;
+  const int nb = base && !kResidual ? nblk * (wave + 1) / kBase - kb0 : 0;
   const int groups = (nb + 3) >> 2;
   char* myw = wring + (base ? wave : 0) * kDWG * kWGroup;
   char* myx = xring + (base ? wave : 0) * kDX * kXSlot;
@@ -714,7 +717,19 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
     }
   }
 
-  if constexpr (kLora) {
+  // Residual form: thread t's two outputs of y (the base), requested now.
+  uint32_t ybase[2] = {0u, 0u};
+  if constexpr (kResidual) {
+    const int tok = threadIdx.x >> 4;
+    if (base && tok < mt) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) ybase[h] = p.y[int64_t(t0 + tok) * p.y_stride + wrow(lo, hi, (threadIdx.x & 15) + 16 * h)];
+    }
+  }
+
+  if constexpr (kResidual) {
+    // (no weight: no decode table)
+  } else if constexpr (kLora) {
     // Waves 0..3: entry t = threadIdx.x of the pair table (and the codebook
     // for the exact decode), from the codebook in scalar registers.
     if (base && wave < 4) {
@@ -757,7 +772,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   // The base waves; the LoRA wave's code follows theirs (so nothing of the
   // streaming state is live across it).
   if (base) {
-  if constexpr (kLora) {
+  if constexpr (kLora && !kResidual) {
     while (*(const volatile __attribute__((address_space(3))) int*)(&table_done) < 4) __builtin_amdgcn_s_sleep(1);
   }
   // A producing wave contracts its part of a single-pass first unit inside
@@ -872,8 +887,10 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   // element r of lane l at r * 64 + l (the delta 1024 floats further).
   {
     float* mine = reinterpret_cast<float*>(myx);
+    if constexpr (!kResidual) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) mine[e * 64 + lane] = acc[e];
+      for (int e = 0; e < 16; ++e) mine[e * 64 + lane] = acc[e];
+    }
     if constexpr (kLora) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) mine[1024 + e * 64 + lane] = dacc[e];
@@ -898,15 +915,18 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
 #pragma unroll
       for (int w = 0; w < kBase; ++w) {
         const float* part = reinterpret_cast<const float*>(xring + w * kDX * kXSlot);
-        sum += part[o];
+        if constexpr (!kResidual) sum += part[o];
         if constexpr (kLora) dsum += part[1024 + o];
       }
+      if constexpr (kResidual) sum = bf16_to_f32(ybase[h]);
       const int row = wrow(lo, hi, col);
       float v = round_bf16(sum);
       if (pe.bias) v = round_bf16(v + bf16_to_f32(pe.bias[row]));
       if (routed) v += round_bf16(dsum * lscale);
       out[h] = round_bf16(v);
-      if (!pe.gated_half && tok < mt) pe.y[int64_t(t0 + tok) * pe.y_stride + row] = uint16_t(f32_to_bf16(v));
+      // (The residual form leaves base-only tokens' y untouched.)
+      if (!pe.gated_half && tok < mt && (!kResidual || routed))
+        pe.y[int64_t(t0 + tok) * pe.y_stride + row] = uint16_t(f32_to_bf16(v));
     }
     // SwiGLU output h = bf16(bf16(silu(gate)) * up) for feature lo + jj (the
     // reference's activation after both LoRA adds, benchmarks/qwen35_decode_silu.py:60-61).
@@ -932,10 +952,10 @@ int64_t static_lds_of(K fn, int64_t& cache) {
 
 // Launches the variant whose static LDS and the waves' scale areas fit one
 // workgroup; returns false when it does not fit.
-template <bool kExact, int kDWG, bool kLora>
+template <bool kExact, int kDWG, bool kLora, bool kResidual = false>
 bool try_launch(dim3 grid, hipStream_t s, const GemvParams& p, int64_t dyn) {
   static int64_t static_lds = -1;
-  auto fn = nf4_decode_wide_kernel<kExact, kDWG, kLora>;
+  auto fn = nf4_decode_wide_kernel<kExact, kDWG, kLora, kResidual>;
   const int64_t st = static_lds_of(fn, static_lds);
   if (st < 0 || st + dyn > kLdsBytes) return false;
   hipLaunchKernelGGL(fn, grid, dim3(64 * (kBase + (kLora ? 1 : 0))), size_t(dyn), s, p);
@@ -1005,6 +1025,39 @@ bool decode_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora) {
   if (n % (8 * kRows)) return false;
   const GemvPlan pl = wide_plan(m, n, k, device_cus(), lora->num_slices * lora->max_rank);
   return pl.units <= 1024 && kPartialsOffset + m * pl.kz * lora->num_slices * lora->max_rank * 8 <= kWorkspaceHeader;
+}
+
+// The residual form (one launch of shrink + expand onto y, no weight) for
+// 33..64 tokens: N a multiple of 256 (whole XCD octets of 32-row groups) and
+// the unit plan's limits.
+bool lora_apply_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora) {
+  if (m <= 32 || m > 64 || n % (8 * kRows)) return false;
+  const GemvPlan pl = wide_plan(m, n, k, device_cus(), lora->num_slices * lora->max_rank);
+  return pl.units <= 1024 && kPartialsOffset + m * pl.kz * lora->num_slices * lora->max_rank * 8 <= kWorkspaceHeader;
+}
+
+int launch_lora_apply_wide(const uint16_t* x, int64_t m, int64_t x_stride, int64_t n, int64_t k, const lf_lora* lora,
+                           uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes, bool withhold,
+                           void* stream) {
+  LF_REQUIRE(lora && lora_apply_wide_fits(m, n, k, lora), "wide LoRA apply: call outside its range");
+  GemvParams p{};
+  p.x = x;
+  p.x_stride = x_stride;
+  p.m = int(m);
+  p.n = int(n);
+  p.k = int(k);
+  p.y = y;
+  p.y_stride = y_stride;
+  p.row_groups = int(n / kRows);
+  p.tiles = int((m + kTokens - 1) / kTokens);
+  const GemvPlan pl = wide_plan(m, n, k, device_cus(), lora->num_slices * lora->max_rank);
+  const int rc = fill_lora_params(p, pl, lora, m, workspace, workspace_bytes, withhold);
+  if (rc != kOk) return rc;
+  const dim3 g3(static_cast<unsigned>(int64_t(p.row_groups) * p.tiles));
+  LF_REQUIRE((try_launch<false, 2, true, true>(g3, static_cast<hipStream_t>(stream), p, 16)),
+             "wide LoRA apply: LDS does not fit");
+  LF_HIP(hipGetLastError());
+  return kOk;
 }
 
 int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,

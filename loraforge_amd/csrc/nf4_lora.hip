@@ -18,6 +18,10 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
                             void* workspace, int64_t workspace_bytes, bool withhold, void* stream);
 int device_cus();
 bool decode_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora);
+bool lora_apply_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora);
+int launch_lora_apply_wide(const uint16_t* x, int64_t m, int64_t x_stride, int64_t n, int64_t k, const lf_lora* lora,
+                           uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes, bool withhold,
+                           void* stream);
 int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                        const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
                        bool exact, bool swiglu, bool withhold, void* stream);
@@ -189,8 +193,12 @@ extern "C" int lf_lora_apply(const uint16_t* x, int64_t m, int64_t x_stride, int
     const int64_t mc = std::min<int64_t>(lf::kDecodeMaxTokens, m - t0);
     lf_lora part = *lora;
     part.token_slots = lora->token_slots + t0;
-    const int rc = lf::launch_nf4_gemv(x + t0 * x_stride, mc, x_stride, &shape, nullptr, &part, y + t0 * y_stride,
-                                       y_stride, workspace, workspace_bytes, false, false, withhold, stream, true);
+    // 33..64 tokens: the wide kernel's residual form where it fits.
+    const int rc = lf::lora_apply_wide_fits(mc, n, k, &part)
+                       ? lf::launch_lora_apply_wide(x + t0 * x_stride, mc, x_stride, n, k, &part, y + t0 * y_stride,
+                                                    y_stride, workspace, workspace_bytes, withhold, stream)
+                       : lf::launch_nf4_gemv(x + t0 * x_stride, mc, x_stride, &shape, nullptr, &part, y + t0 * y_stride,
+                                             y_stride, workspace, workspace_bytes, false, false, withhold, stream, true);
     if (rc != lf::kOk) return rc;
   }
   return lf::kOk;
