@@ -30,6 +30,10 @@ benchmarks/check_qwen35_nf4_ops.py:11-41):
               (ranks {4..64}), Zipf(1.1) routing;
   c5          prefill M = 2048, K = 4096, N = 11008, NF4 + double quant,
               8 segments of rank 32 (TFLOP/s against 2.5 PFLOP/s);
+  fleet       the Fleet row_expand at the reference's row-tile study shapes
+              (docs/qwen35.md:379-386): 32 tokens over four mixed-rank
+              adapters, 1024 output columns and QKV 4096/512/512 (warm: the
+              same tensors every call, as there);
   dequant     standalone NF4 dequantisation 8192 x 1024 (the reference's
               published operator screen).
 ``cpu_baseline`` is the reference's chain in PyTorch on the host cores.
@@ -553,6 +557,49 @@ def c5_items(device, reps: int):
     return items, {"c5": meta, "c5_base_only": dict(meta, lora=False)}
 
 
+FLEET_SHAPES = (
+    # (name, slice widths, retained ranks of slots 1..4): the reference's row-tile study
+    # (docs/qwen35.md:379-386, benchmarks/rowexpand_tiles.py:38-42), 32 tokens routed 1,2,3,4,1,...
+    ("fleet_out_proj_1024", (1024,), (8, 16, 32, 64)),
+    ("fleet_qkv_4096_512_512", (4096, 512, 512), (32, 64, 64, 64)),
+)
+
+
+def fleet_items(device, reps: int, tokens: int = 32, capacity: int = 64):
+    """The Fleet ``row_expand`` at the reference's published shapes (warm: the same tensors every call)."""
+    import numpy as np
+    import torch
+
+    from loraforge_amd.ops import rowexpand
+
+    items, meta = [], {}
+    g = torch.Generator(device="cpu").manual_seed(411)
+    routes = [1 + t % 4 for t in range(tokens)]
+    indptr, seg_slots, order = segments_of(routes)
+    i32 = dict(dtype=torch.int32, device=device)
+    for name, widths, retained in FLEET_SHAPES:
+        n, slices = sum(widths), len(widths)
+        ranks = np.array((0,) + retained, np.int32)
+        sizes = n * ranks
+        offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+        store = (torch.randn(int(sizes.sum()) + 8, generator=g) / 20).bfloat16().to(device)
+        z = (torch.randn(tokens, slices * capacity, generator=g) / 10).bfloat16().to(device)
+        y = (torch.randn(tokens, n, generator=g) / 10).bfloat16().to(device)
+        args = (
+            z, store, torch.from_numpy(offsets).to(device), torch.from_numpy(ranks).to(device), y,
+            torch.from_numpy(indptr).to(device), torch.from_numpy(seg_slots).to(device),
+            torch.from_numpy(order).to(device), torch.from_numpy(ranks).to(device),
+            torch.tensor([0.0, 1.0, 0.75, 1.25, 0.5], device=device),
+            torch.tensor(np.concatenate([[0], np.cumsum(widths)]), **i32),
+            torch.tensor([len(seg_slots)], **i32), capacity,
+        )
+        used = [int(ranks[s]) for s in routes]
+        work = sum(2 * n * int(r) for r in retained) + sum(2 * slices * r for r in used) + 2 * 2 * tokens * n
+        items.append(Timed(name, [lambda a=args: rowexpand.row_expand(*a)] * 8, reps, work))
+        meta[name] = dict(tokens=tokens, widths=list(widths), ranks=list(retained), segments=len(seg_slots), op="row_expand")
+    return items, meta
+
+
 def dequant_items(device, reps: int, copies: int = 64):
     """Standalone NF4 dequantisation of an 8192 x 1024 weight (bf16 out), over 64 weight copies."""
     import torch
@@ -610,7 +657,7 @@ def main() -> int:
     parser.add_argument("--batch", type=int, default=64)
     parser.add_argument("--only", action="store_true", help="headline decode only (no configs/CPU)")
     parser.add_argument("--no-cpu", action="store_true")
-    parser.add_argument("--configs", default="all", help="comma list of c1,north_star,c2,c3,c4,c5,dequant (default all)")
+    parser.add_argument("--configs", default="all", help="comma list of c1,north_star,c2,c3,c4,c5,fleet,dequant (default all)")
     parser.add_argument("--reps", type=int, default=10, help="graph replays per round for each config")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     args = parser.parse_args()
@@ -670,7 +717,7 @@ def main() -> int:
         },
     }
     if not args.only:
-        wanted = set(args.configs.split(",")) if args.configs != "all" else {"c1", "north_star", "c2", "c3", "c4", "c5", "dequant"}
+        wanted = set(args.configs.split(",")) if args.configs != "all" else {"c1", "north_star", "c2", "c3", "c4", "c5", "fleet", "dequant"}
         items, meta = [], {}
         if wanted & {"c1", "north_star", "c2"}:
             it, me = decode_items(work, args.reps, wanted)
@@ -686,6 +733,10 @@ def main() -> int:
             meta.update(me)
         if "c5" in wanted:
             it, me = c5_items(device, max(2, args.reps // 2))
+            items += it
+            meta.update(me)
+        if "fleet" in wanted:
+            it, me = fleet_items(device, args.reps)
             items += it
             meta.update(me)
         if "dequant" in wanted:

@@ -25,8 +25,9 @@ extern "C" {
 
 /* 2: lf_row_shrink gained num_adapters, workspace, workspace_bytes and flags,
  * lf_row_expand gained segments (arguments inserted mid-list).
- * 3: lf_lora gained num_slots (appended). */
-#define LF_ABI_VERSION 3
+ * 3: lf_lora gained num_slots (appended).
+ * 4: lf_row_expand_tiled added. */
+#define LF_ABI_VERSION 4
 #define LF_OK 0
 #define LF_EINVAL 1
 #define LF_EHIP 2
@@ -109,6 +110,22 @@ int lf_row_expand(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets
                   const float* scales, const int32_t* slice_offsets, const int32_t* segment_count,
                   int64_t segments, int64_t tokens, int64_t out_width, int64_t y_stride,
                   int32_t num_slices, int64_t capacity, int32_t blocks, int32_t threads, void* stream);
+
+/* lf_row_expand_tiled replaces the pybind `expand` of ops/csrc/rowexpand.cu:98-127
+ * (the Fleet row_expand, ops/rowexpand.py:42-92): lf_row_expand's arguments
+ * plus row_tile (2, 4, 8 or 16; anything else is LF_EINVAL, as there). The
+ * reference splits a segment's B work into items of row_tile tokens; here an
+ * item is a segment times a run of output columns, and row_tile bounds that
+ * run: 16 lets the library pick it from the work count (as lf_row_expand
+ * does), 8 caps it at 32 columns per wave, 4 and 2 at 16. Outputs are
+ * bitwise identical for every row_tile. */
+int lf_row_expand_tiled(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets,
+                        const int32_t* b_strides, uint16_t* y, const int32_t* segment_indptr,
+                        const int32_t* segment_slots, const int32_t* token_indices, const int32_t* ranks,
+                        const float* scales, const int32_t* slice_offsets, const int32_t* segment_count,
+                        int64_t segments, int64_t tokens, int64_t out_width, int64_t y_stride,
+                        int32_t num_slices, int64_t capacity, int32_t blocks, int32_t threads, int32_t row_tile,
+                        void* stream);
 
 /* --------------------------------------------------------------------------
  * Fused NF4 base linear + per-token multi-LoRA (one launch for decode).

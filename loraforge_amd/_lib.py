@@ -24,7 +24,7 @@ LF_PLAN_DECODE_CHUNKS = 4
 LF_PLAN_PREFILL = 8
 LF_TEST_WITHHOLD_PARTIALS = 0x100
 NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _handle: ctypes.CDLL | None = None
@@ -92,6 +92,10 @@ _PROTOTYPES = {
     "lf_row_expand": (
         ctypes.c_int,
         [c_void_p] * 12 + [c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, c_int32, c_void_p],
+    ),
+    "lf_row_expand_tiled": (
+        ctypes.c_int,
+        [c_void_p] * 12 + [c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int32, c_int32, c_int32, c_void_p],
     ),
     "lf_nf4_lora_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int32, c_int32]),
     "lf_nf4_lora_linear": (

@@ -257,7 +257,6 @@ __global__ __launch_bounds__(kShrinkThreads) void row_shrink_kernel(ShrinkArgs p
 }
 
 // ------------------------------- expand ----------------------------------
-constexpr int kTilesPerWave = 4;
 constexpr int kZPitch = 72;  // bf16 per staged z row (64 + 8: rows land on different banks)
 
 struct ExpandArgs {
@@ -309,7 +308,7 @@ __device__ __forceinline__ uint4 b_mask(uint4 q, int st, int r, int k) {
 // Loads are grouped into three dependent rounds per item: the segment's
 // bounds and slot; the slot's metadata and the token ids; then B, z and the
 // y values the tile will update, all together. Only then LDS, MFMA, stores.
-template <int kWaves>
+template <int kWaves, int kTilesPerWave>
 __global__ __launch_bounds__(64 * kWaves) void row_expand_kernel(ExpandArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t zs[kMaxSlices][kMaxSegment][kZPitch];
   constexpr int kCols = 16 * kTilesPerWave * kWaves;  // output columns per item
@@ -564,34 +563,93 @@ extern "C" int lf_row_shrink(const uint16_t* x, const uint16_t* a, uint16_t* z, 
   return lf::kOk;
 }
 
+namespace lf {
+namespace {
+
+// The widest item (tiles of 16 columns per wave, at most max_tiles) that
+// still gives one item per CU; narrower items otherwise. Narrow outputs with
+// few segments are latency chains that only more workgroups shorten (C32,
+// four adapters: 1024 columns 6.2 -> 4.3 us with 64-column items, QKV
+// 4096/512/512 6.5 -> 4.6 us); with enough segments the wide items win
+// (c2, 4096 columns: 14.4 us against 18.1 us), since every item stages its
+// segment's z once.
+int expand_tiles(int64_t segments, int64_t n, int waves, int max_tiles) {
+  int tiles = max_tiles;
+  while (tiles > 1 && segments * ((n + 16 * tiles * waves - 1) / (16 * tiles * waves)) < 256) tiles /= 2;
+  return tiles;
+}
+
+int row_expand_launch(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets, const int32_t* b_strides,
+                      uint16_t* y, const int32_t* segment_indptr, const int32_t* segment_slots,
+                      const int32_t* token_indices, const int32_t* ranks, const float* scales,
+                      const int32_t* slice_offsets, const int32_t* segment_count, int64_t segments, int64_t tokens,
+                      int64_t out_width, int64_t y_stride, int32_t num_slices, int64_t capacity, int32_t blocks,
+                      int32_t threads, int max_tiles, void* stream) {
+  LF_REQUIRE(tokens >= 0 && tokens < (int64_t(1) << 31), "tokens out of range");
+  if (tokens == 0) return kOk;
+  LF_REQUIRE(z && b && b_offsets && b_strides && y && segment_indptr && segment_slots && token_indices && ranks &&
+                 scales && slice_offsets && segment_count,
+             "null pointer argument");
+  LF_REQUIRE(num_slices >= 1 && num_slices <= kMaxSlices, "num_slices must be in 1..4");
+  LF_REQUIRE(out_width > 0 && out_width < (int64_t(1) << 31) && y_stride >= out_width, "invalid output width/stride");
+  LF_REQUIRE(capacity >= 1 && capacity * num_slices < (int64_t(1) << 31), "capacity out of range");
+  LF_REQUIRE(threads == 128 || threads == 256, "threads must be 128 or 256");
+  LF_REQUIRE(blocks >= 1 && blocks <= 65535, "blocks must be in 1..65535");
+  LF_REQUIRE(aligned16(b), "B store must be 16-byte aligned");
+  LF_REQUIRE(segments >= 0 && segments * ((out_width + 31) / 32) < (int64_t(1) << 31), "segment work count out of range");
+  if (segments == 0) return kOk;
+  ExpandArgs p{z, b, b_offsets, b_strides, y, segment_indptr, segment_slots, token_indices, ranks, scales,
+               slice_offsets, segment_count, int(segments), int(out_width), int(num_slices), int(capacity), y_stride,
+               (out_width % 4 == 0 && y_stride % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0) ? 1 : 0,
+               (capacity * num_slices % 4 == 0 && reinterpret_cast<uintptr_t>(z) % 8 == 0) ? 1 : 0};
+  auto s = static_cast<hipStream_t>(stream);
+  const int waves = threads / 64;
+  const int tiles = expand_tiles(segments, out_width, waves, max_tiles);
+  // Workgroups past the item count would only read the slice bounds and exit.
+  const int64_t cols = 16 * tiles * waves;
+  blocks = int32_t(std::min<int64_t>(blocks, segments * ((out_width + cols - 1) / cols)));
+  if (waves == 4) {
+    if (tiles == 1)
+      hipLaunchKernelGGL((row_expand_kernel<4, 1>), dim3(blocks), dim3(256), 0, s, p);
+    else if (tiles == 2)
+      hipLaunchKernelGGL((row_expand_kernel<4, 2>), dim3(blocks), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((row_expand_kernel<4, 4>), dim3(blocks), dim3(256), 0, s, p);
+  } else {
+    if (tiles == 1)
+      hipLaunchKernelGGL((row_expand_kernel<2, 1>), dim3(blocks), dim3(128), 0, s, p);
+    else if (tiles == 2)
+      hipLaunchKernelGGL((row_expand_kernel<2, 2>), dim3(blocks), dim3(128), 0, s, p);
+    else
+      hipLaunchKernelGGL((row_expand_kernel<2, 4>), dim3(blocks), dim3(128), 0, s, p);
+  }
+  LF_HIP(hipGetLastError());
+  return kOk;
+}
+
+}  // namespace
+}  // namespace lf
+
 extern "C" int lf_row_expand(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets,
                              const int32_t* b_strides, uint16_t* y, const int32_t* segment_indptr,
                              const int32_t* segment_slots, const int32_t* token_indices, const int32_t* ranks,
                              const float* scales, const int32_t* slice_offsets, const int32_t* segment_count,
                              int64_t segments, int64_t tokens, int64_t out_width, int64_t y_stride,
                              int32_t num_slices, int64_t capacity, int32_t blocks, int32_t threads, void* stream) {
-  LF_REQUIRE(tokens >= 0 && tokens < (int64_t(1) << 31), "tokens out of range");
-  if (tokens == 0) return lf::kOk;
-  LF_REQUIRE(z && b && b_offsets && b_strides && y && segment_indptr && segment_slots && token_indices && ranks &&
-                 scales && slice_offsets && segment_count,
-             "null pointer argument");
-  LF_REQUIRE(num_slices >= 1 && num_slices <= lf::kMaxSlices, "num_slices must be in 1..4");
-  LF_REQUIRE(out_width > 0 && out_width < (int64_t(1) << 31) && y_stride >= out_width, "invalid output width/stride");
-  LF_REQUIRE(capacity >= 1 && capacity * num_slices < (int64_t(1) << 31), "capacity out of range");
-  LF_REQUIRE(threads == 128 || threads == 256, "threads must be 128 or 256");
-  LF_REQUIRE(blocks >= 1 && blocks <= 65535, "blocks must be in 1..65535");
-  LF_REQUIRE(lf::aligned16(b), "B store must be 16-byte aligned");
-  LF_REQUIRE(segments >= 0 && segments * ((out_width + 255) / 64) < (int64_t(1) << 31), "segment work count out of range");
-  if (segments == 0) return lf::kOk;
-  lf::ExpandArgs p{z, b, b_offsets, b_strides, y, segment_indptr, segment_slots, token_indices, ranks, scales,
-                   slice_offsets, segment_count, int(segments), int(out_width), int(num_slices), int(capacity), y_stride,
-                   (out_width % 4 == 0 && y_stride % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 8 == 0) ? 1 : 0,
-                   (capacity * num_slices % 4 == 0 && reinterpret_cast<uintptr_t>(z) % 8 == 0) ? 1 : 0};
-  auto s = static_cast<hipStream_t>(stream);
-  if (threads == 256)
-    hipLaunchKernelGGL(lf::row_expand_kernel<4>, dim3(blocks), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(lf::row_expand_kernel<2>, dim3(blocks), dim3(128), 0, s, p);
-  LF_HIP(hipGetLastError());
-  return lf::kOk;
+  return lf::row_expand_launch(z, b, b_offsets, b_strides, y, segment_indptr, segment_slots, token_indices, ranks,
+                               scales, slice_offsets, segment_count, segments, tokens, out_width, y_stride, num_slices,
+                               capacity, blocks, threads, 4, stream);
+}
+
+extern "C" int lf_row_expand_tiled(const uint16_t* z, const uint16_t* b, const int64_t* b_offsets,
+                                   const int32_t* b_strides, uint16_t* y, const int32_t* segment_indptr,
+                                   const int32_t* segment_slots, const int32_t* token_indices, const int32_t* ranks,
+                                   const float* scales, const int32_t* slice_offsets,
+                                   const int32_t* segment_count, int64_t segments, int64_t tokens,
+                                   int64_t out_width, int64_t y_stride, int32_t num_slices, int64_t capacity,
+                                   int32_t blocks, int32_t threads, int32_t row_tile, void* stream) {
+  LF_REQUIRE(row_tile == 2 || row_tile == 4 || row_tile == 8 || row_tile == 16, "row_tile must be 2, 4, 8, or 16");
+  return lf::row_expand_launch(z, b, b_offsets, b_strides, y, segment_indptr, segment_slots, token_indices, ranks,
+                               scales, slice_offsets, segment_count, segments, tokens, out_width, y_stride, num_slices,
+                               capacity, blocks, threads, row_tile >= 16 ? 4 : row_tile == 8 ? 2 : 1, stream);
 }

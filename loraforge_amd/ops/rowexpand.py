@@ -3,11 +3,15 @@
 Reference: ``src/loraforge/ops/rowexpand.py:34-92`` (``direct_shrink``,
 ``row_expand``) over ``ops/csrc/rowexpand.cu:87-127``. The arithmetic is the
 retained-rank shrink/expand of ``lora_rows`` (same rounding chain), with the
-Fleet argument order, up to four slices and the ``row_tile`` knob: the
-reference splits segments into row tiles of 2/4/8/16 inside its B kernel and
-documents the outputs as bitwise-equal to the untiled kernel, so the value is
-validated and the one gfx950 kernel serves every tile size. Both calls go to
-the same C entry points as ``lora_rows`` (``lf_row_shrink``, ``lf_row_expand``).
+Fleet argument order, up to four slices and the ``row_tile`` knob. The
+reference splits a segment's B work into items of 2/4/8/16 token rows and
+documents the outputs as bitwise-equal to the untiled kernel; here an item is
+a segment times a run of output columns (the MFMA tile covers all 16 tokens of
+a segment), and ``row_tile`` bounds that run: 16 lets the library choose it
+from the work count, 8 caps it at 128 columns (256 threads), 4 and 2 at 64.
+Outputs are bitwise identical for every value. ``direct_shrink`` goes to
+``lf_row_shrink`` (as ``lora_rows.row_shrink`` does), ``row_expand`` to
+``lf_row_expand_tiled``.
 """
 
 from __future__ import annotations
@@ -164,7 +168,7 @@ def row_expand(
     lib = _lib.library()
     with torch.cuda.device(z.device):
         _lib.check(
-            lib.lf_row_expand(
+            lib.lf_row_expand_tiled(
                 z.data_ptr(),
                 store.data_ptr(),
                 offsets.data_ptr(),
@@ -185,6 +189,7 @@ def row_expand(
                 capacity,
                 blocks,
                 threads,
+                row_tile,
                 _lib.stream_of(z.device),
             )
         )

@@ -53,6 +53,35 @@ def test_fleet_shrink_and_tiled_expand(slices, device):
         assert torch.equal(ref, outs[0])
 
 
+@pytest.mark.parametrize("threads", [128, 256])
+def test_fleet_item_widths_give_identical_bits(threads, device):
+    """5700 output columns over 12 segments: row_tile 16 runs the widest items
+    (64 columns per wave), 8 at most 32 and 4 / 2 at most 16; every variant must
+    give the bits of ``lora_rows.row_expand`` and meet the oracle."""
+    slices = 3
+    c = _cases.row_case(slices, columns=1900, seed=275)
+    x, a, z, b, _, output, routes, meta = gpu_case(c, device)
+    before = output.clone()
+    rowexpand.direct_shrink(x, a, z, routes, meta["ranks"], slices, 64)
+    torch.cuda.synchronize()
+    zb = bits(z)
+    outs = []
+    for tile in (16, 8, 4, 2):
+        out = before.clone()
+        rowexpand.row_expand(
+            z, b, meta["b_offsets"], meta["b_strides"], out, meta["segment_indptr"], meta["segment_slots"],
+            meta["token_indices"], meta["ranks"], meta["scales"], meta["slice_offsets"], meta["segment_count"],
+            z.shape[1] // slices, row_tile=tile, threads=threads,
+        )
+        outs.append(out)
+    ref = before.clone()
+    lora_row_expand(z, b, ref, **meta, threads=threads)
+    torch.cuda.synchronize()
+    for out in outs:
+        assert torch.equal(out, ref)
+    close(bits(ref), rows.row_expand(zb, c["b"], bits(before), **c["meta"]))
+
+
 def test_fleet_contract_errors(device):
     c = _cases.row_case(1, seed=15)
     x, a, z, b, _, output, routes, meta = gpu_case(c, device)
