@@ -29,7 +29,10 @@ benchmarks/check_qwen35_nf4_ops.py:11-41):
   c4          NF4 4096^2, 256 tokens, 128 retained-rank adapters
               (ranks {4..64}), Zipf(1.1) routing;
   c5          prefill M = 2048, K = 4096, N = 11008, NF4 + double quant,
-              8 segments of rank 32 (TFLOP/s against 2.5 PFLOP/s);
+              8 segments of rank 32 (TFLOP/s against 2.5 PFLOP/s); c5_swiglu
+              reads the weight as a merged gate/up projection (two rank-32
+              slices) with the SwiGLU in the GEMM's epilogue, against the
+              linear followed by silu_mul (c5_swiglu_two_launches);
   fleet       the Fleet row_expand at the reference's row-tile study shapes
               (docs/qwen35.md:379-386): 32 tokens over four mixed-rank
               adapters, 1024 output columns and QKV 4096/512/512 (warm: the
@@ -549,12 +552,41 @@ def c5_items(device, reps: int):
     out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
     flops_base = 2 * m * n * k
     flops = flops_base + 2 * m * k * rank + 2 * m * rank * n
+    # The same weight read as a merged gate/up projection (5504 + 5504 rows) with two
+    # rank-32 slices per segment: the SwiGLU output in the GEMM's epilogue, against the
+    # linear followed by silu_mul.
+    from loraforge_amd.ops.activation import silu_mul
+
+    lora2 = LoraBatch(
+        (torch.randn(segs * 2 * rank * k, generator=g) * 0.02).bfloat16().to(device),
+        torch.arange(segs, **i64) * (2 * rank * k),
+        b,
+        torch.arange(segs, **i64) * (n * rank),
+        torch.full((segs,), rank, dtype=torch.int32, device=device),
+        torch.full((segs,), rank, dtype=torch.int32, device=device),
+        torch.full((segs,), 2.0, device=device),
+        slots,
+        torch.tensor([0, n // 2, n], dtype=torch.int32, device=device),
+        max_rank=rank,
+    )
+    h = torch.empty(m, n // 2, dtype=torch.bfloat16, device=device)
+
+    def two_launches():
+        nf4_lora_linear(x, q, st, lora=lora2, out=out)
+        silu_mul(out, out=h)
+
+    flops_swiglu = flops_base + 2 * m * k * 2 * rank + 2 * m * rank * n
     items = [
         Timed("c5", [lambda: nf4_lora_linear(x, q, st, lora=lora, out=out)] * 4, reps, flops, unit="TFLOP/s"),
         Timed("c5_base_only", [lambda: nf4_lora_linear(x, q, st, out=out)] * 4, reps, flops_base, unit="TFLOP/s"),
+        Timed("c5_swiglu", [lambda: nf4_lora_linear(x, q, st, lora=lora2, out=h, swiglu=True)] * 4, reps, flops_swiglu,
+              unit="TFLOP/s"),
+        Timed("c5_swiglu_two_launches", [two_launches] * 4, reps, flops_swiglu, unit="TFLOP/s"),
     ]
     meta = dict(m=m, n=n, k=k, segments=segs, rank=rank, double_quant=True, segment_lengths=lengths.tolist())
-    return items, {"c5": meta, "c5_base_only": dict(meta, lora=False)}
+    sw = dict(meta, gate_up=[n // 2, n // 2], slices=2, swiglu=True)
+    return items, {"c5": meta, "c5_base_only": dict(meta, lora=False), "c5_swiglu": dict(sw, launches=1),
+                   "c5_swiglu_two_launches": dict(sw, launches=2)}
 
 
 FLEET_SHAPES = (

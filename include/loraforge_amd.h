@@ -199,13 +199,14 @@ int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_
  * flags: LF_EXACT_WEIGHTS makes the decode kernel multiply the same exact
  * weights; by default it contracts bf16(code) and applies each fp32 block
  * scale to the block's MFMA sum. The prefill GEMM ignores the flag.
- * LF_SWIGLU_OUTPUT (decode, M <= 64, N a multiple of 32): the weight is a
- * merged gate/up projection (gate rows 0 .. N/2, up rows N/2 .. N; with LoRA
- * its two slices are [0, N/2, N]) and y receives
- * h[m][f] = bf16(bf16(silu(gate[m][f])) * up[m][f]), [M, N/2] with row
- * stride y_stride >= N/2, where gate and up are the bf16 outputs including
- * their LoRA adds (benchmarks/qwen35_decode_silu.py:60-61, fused into the
- * epilogue instead of a second launch). */
+ * LF_SWIGLU_OUTPUT (any M; the prefill GEMM also needs y 16-byte aligned
+ * with y_stride % 8 == 0): the weight is a merged gate/up projection (gate
+ * rows 0 .. N/2, up rows N/2 .. N; with LoRA its two slices are
+ * [0, N/2, N]) and y receives h[m][f] = bf16(bf16(silu(gate[m][f])) *
+ * up[m][f]), [M, N/2] with row stride y_stride >= N/2, where gate and up are
+ * the bf16 outputs including their LoRA adds (benchmarks/qwen35_decode_silu.py:60-61
+ * and the prefill expand_act_kernel, benchmarks/qwen35_prefill_fused.py:14-93,
+ * fused into the epilogue instead of a second launch). */
 #define LF_EXACT_WEIGHTS 1
 #define LF_SWIGLU_OUTPUT 2
 #define LF_PLAN_DECODE_CHUNKS 4

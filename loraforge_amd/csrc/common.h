@@ -65,6 +65,42 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float a) { return pack_bf16x2(a,
 // fp32 -> nearest bf16 value, returned as fp32.
 __device__ __forceinline__ float round_bf16(float a) { return bf16_to_f32(f32_to_bf16(a)); }
 
+// bf16(silu(g)) * u in fp32 (the caller's store rounds the product to bf16),
+// silu(g) = g / (1 + e^-g) as the reference's activation
+// (benchmarks/qwen35_decode_silu.py:60-61), in about 13 instructions instead
+// of about 30 for expf and an IEEE division:
+//  - e^-g = 2^(t + lo) = 2^t (1 + lo ln 2) with t = fl(-c log2 e) and lo the
+//    rounding error of t plus c times the tail of log2 e (Cody-Waite), 2^t
+//    from the hardware exp2 (1 ulp); c is g clamped to [-126, 126], which
+//    changes nothing past the clamp (there e^-g is 0 or overflows either
+//    way) and keeps t and lo finite for every g;
+//  - the quotient from the hardware reciprocal refined by one Newton step,
+//    with the divisor scaled by 2^-64 above 2^64 (the reciprocal flushes
+//    results below 2^-126 to zero, though g / d is still a normal number up
+//    to d near 2^128), skipped where 1 + e^-g overflowed (g below about
+//    -88.7: silu -0, as g / inf) or the quotient is infinite; silu has the
+//    sign of g, which also keeps -0 for g = -0.
+// Every SwiGLU path (lf_swiglu and the fused decode and prefill epilogues)
+// uses this one function, so a fused activation and the linear followed by
+// lf_swiglu give identical bits.
+__device__ __forceinline__ float silu_times(float g, float u) {
+  constexpr float kNegLog2eHi = -1.44269502162933349609375f;    // -log2(e) rounded to fp32
+  constexpr float kNegLog2eLo = -1.925963033500011079e-08f;      // -log2(e) - kNegLog2eHi
+  constexpr float kLn2 = 0.693147180559945309f;
+  const float c = __builtin_fminf(__builtin_fmaxf(g, -126.0f), 126.0f);
+  const float t = c * kNegLog2eHi;
+  const float lo = fmaf(c, kNegLog2eLo, fmaf(c, kNegLog2eHi, -t));
+  const float e = __builtin_amdgcn_exp2f(t) * fmaf(lo, kLn2, 1.0f);
+  const float d = 1.0f + e;
+  const float sc = d > 0x1p64f ? 0x1p-64f : 1.0f;
+  const float ds = d * sc;
+  const float r = __builtin_amdgcn_rcpf(ds);
+  const float q = g * r;  // g / d / sc
+  const bool refine = d < __builtin_huge_valf() && __builtin_fabsf(q) < __builtin_huge_valf();
+  const float act = __builtin_copysignf((refine ? fmaf(fmaf(-q, ds, g), r, q) : q) * sc, g);
+  return round_bf16(act) * u;
+}
+
 // One 16x16x32 bf16 MFMA step: acc[i = 4*(lane/16) + r][j = lane%16] +=
 // sum_k a[i][k] * b[k][j], where lane l supplies a[l%16][8*(l/16) .. +8)
 // and b[8*(l/16) .. +8)[l%16].

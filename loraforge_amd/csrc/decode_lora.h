@@ -16,13 +16,6 @@
 namespace lf {
 namespace {
 
-// bf16(silu(g)) * u in fp32 (the caller's store rounds the product): silu
-// as g / (1 + e^-g), the form of the reference's activation.
-__device__ __forceinline__ float silu_times(float g, float u) {
-  const float act = g / (1.0f + expf(-g));
-  return round_bf16(act) * u;
-}
-
 // Global output row of local row j (0 .. R - 1) of a row group whose first
 // R / 2 rows start at lo and the others at hi (hi = lo + R / 2 for a plain
 // group; in SwiGLU-output mode lo is the group's first gate row and hi the

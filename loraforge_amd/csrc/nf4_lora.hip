@@ -15,7 +15,7 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
 int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int max_rank);
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                            void* workspace, int64_t workspace_bytes, bool withhold, void* stream);
+                            void* workspace, int64_t workspace_bytes, bool swiglu, bool withhold, void* stream);
 int device_cus();
 bool decode_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora);
 bool lora_apply_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora);
@@ -104,8 +104,7 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
   LF_REQUIRE(lf::aligned16(x) && x_stride >= k && x_stride % 8 == 0, "x must be 16-byte aligned with row stride %% 8 == 0");
   LF_REQUIRE(lf::aligned16(w->qweight), "packed weight must be 16-byte aligned");
   LF_REQUIRE(y_stride >= (swiglu ? n / 2 : n), "output row stride must cover the output width");
-  LF_REQUIRE(!swiglu || (m <= lf::kDecodeMaxTokens && n % 32 == 0),
-             "SwiGLU output needs a decode batch (M <= 64) and N a multiple of 32");
+  LF_REQUIRE(!swiglu || n % 64 == 0, "SwiGLU output needs N a multiple of 64");
   LF_REQUIRE(!swiglu || !lora || lora->num_slices == 2, "SwiGLU output with LoRA needs the two gate/up slices");
   if (lora) {
     LF_REQUIRE(lora->num_slices >= 1 && lora->num_slices <= 3, "num_slices must be in 1..3");
@@ -141,7 +140,7 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
   }
   if (!chunked)
     return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
-                                       withhold, stream);
+                                       swiglu, withhold, stream);
   // 64-token chunks in token order on the caller's stream; each is one decode
   // launch over its rows of x, y and the token routes.
   for (int64_t t0 = 0; t0 < m; t0 += lf::kDecodeMaxTokens) {
@@ -152,7 +151,7 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
       part.token_slots = lora->token_slots + t0;
     }
     const int rc = lf::launch_decode(x + t0 * x_stride, mc, x_stride, w, bias, lora ? &part : nullptr,
-                                     y + t0 * y_stride, y_stride, workspace, workspace_bytes, exact, false, withhold,
+                                     y + t0 * y_stride, y_stride, workspace, workspace_bytes, exact, swiglu, withhold,
                                      stream);
     if (rc != lf::kOk) return rc;
   }

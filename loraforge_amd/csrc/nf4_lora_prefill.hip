@@ -530,9 +530,20 @@ __device__ __forceinline__ void round_bias(const PrefillParams& p, f32x4 (&acc)[
     }
 }
 
+// Weight row of tile row r (0 .. kBN - 1) in column tile nt. SwiGLU output:
+// tile nt produces activation columns kBN/2 nt .. + kBN/2; its rows below
+// kBN/2 are the gate rows of those columns, the others the matching up rows
+// (n / 2 further on), so a wave's 48 rows stay contiguous.
+template <bool kSwiglu>
+__device__ __forceinline__ int tile_row(const PrefillParams& p, int nt, int r) {
+  if constexpr (!kSwiglu) return nt * kBN + r;
+  constexpr int kHalf = kBN / 2;
+  return r < kHalf ? nt * kHalf + r : (p.n >> 1) + nt * kHalf + (r - kHalf);
+}
+
 // Block ids below mtiles * zparts (LoRA launches only) produce the tiles' z
 // rows; the others are GEMM tiles, M-tile b % mtiles on consecutive ids.
-template <bool kLora>
+template <bool kLora, bool kSwiglu>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   __shared__ __attribute__((aligned(16))) char xring[kXD * kXBytes];
   __shared__ __attribute__((aligned(16))) uint4 wdec[2][kBN * 8];
@@ -574,7 +585,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   WLane wl;
 #pragma unroll
   for (int i = 0; i < kDw; ++i) {
-    const int nrow = min(n0 + (tid >> 3) + 64 * i, p.n - 1);
+    const int nrow = min(tile_row<kSwiglu>(p, nt, (tid >> 3) + 64 * i), p.n - 1);
     wl.qoff[i] = uint32_t(int64_t(nrow) * (p.k >> 1) + (tid & 7) * 4);
     wl.soff[i] = uint32_t(int64_t(nrow) * (p.k / kNf4Block) * 4);
   }
@@ -728,7 +739,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   // ---- epilogue: acc[i][j][e] = C[token m0 + wm*128 + 16i + c][feature n0 + wn*48 + 16j + 4g + e]
   // (W is the MFMA's A operand, so a lane holds four consecutive features of
   // one token: one 8-byte store per fragment).
-  const int wn0 = n0 + wn * 48;
+  const int wn0 = tile_row<kSwiglu>(p, nt, wn * 48);
   if constexpr (kLora) {
     // z rows of slice 0 and the B fragments of the first slot are requested
     // before the base rounding, so their latency overlaps it.
@@ -788,13 +799,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
     int dq[kAhead + 1];
     uint4 bq0[kAhead + 1][kJ], bq1[kAhead + 1][kJ];
     wait_z(p, mt, tag, tslot, list, order, mrank, mstride, mscale, mboff, reinterpret_cast<float*>(xring), zmissing);
-    uint4* zs = reinterpret_cast<uint4*>(xring);  // [token][8 units] with the x swizzle (the ring is idle)
+    // Every slice's z rows are staged at once (slice s at unit s * kBM * 8 of
+    // the idle x ring: [token][8 units] with the x swizzle), so after one
+    // barrier each wave applies exactly the slices its 48 columns touch,
+    // without waiting at a barrier through the expand of a slice it does not
+    // take (a SwiGLU tile's gate and up waves take different slices).
+    static_assert(3 * kBM * 8 * 16 <= kXD * kXBytes, "the z rows of three slices (the most a call has) fit the x ring");
+    uint4* zs_all = reinterpret_cast<uint4*>(xring);
     for (int s = 0; s < p.slices; ++s) {
-      const int lo = p.slice_offsets[s];
-      const int hi = p.slice_offsets[s + 1];
-      if (s > 0) __syncthreads();  // the previous slice's readers of zs are done
       // The slice's z rows (the one place these untracked loads are made), and
-      // for slice 0 the first slot's B, requested before the base rounding.
+      // with slice 0 the first slot's B, requested before the base rounding.
       load_zs(s);
       if (s == 0) {
         if (first < nd) request_b(first, bq0[0], bq1[0]);
@@ -806,16 +820,24 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
 #pragma unroll
       for (int q = 0; q < kZq; ++q) {
         const int row = (tid >> 3) + (kThreads / 8) * q;
-        zs[swz(row, tid & 7)] = tslot[row] >= 0 ? make_uint4(zr[q].x, zr[q].y, zr[q].z, zr[q].w) : make_uint4(0, 0, 0, 0);
+        zs_all[s * kBM * 8 + swz(row, tid & 7)] =
+            tslot[row] >= 0 ? make_uint4(zr[q].x, zr[q].y, zr[q].z, zr[q].w) : make_uint4(0, 0, 0, 0);
       }
-      __syncthreads();
+    }
+    __syncthreads();
+    bool b_first_ready = true;  // the B of `first` requested above is still unused
+    for (int s = 0; s < p.slices; ++s) {
+      const int lo = p.slice_offsets[s];
+      const int hi = p.slice_offsets[s + 1];
       if (hi <= wn0 || lo >= wn0 + 48) continue;  // this wave's 48 columns miss the slice
       const bool inside = lo <= wn0 && wn0 + 48 <= hi;
+      const uint4* zs = zs_all + s * kBM * 8;
       // delta[n][m] = sum_j B_g[n][j] z[m][j] for the wave's 128 tokens x 48
       // features, added with the reference's two roundings to the tokens
       // routed to g and the features of slice s. The B of the next kAhead
       // live slots is in flight while this slot's MFMAs run.
-      if (s > 0 && first < nd) request_b(first, bq0[0], bq1[0]);
+      if (!b_first_ready && first < nd) request_b(first, bq0[0], bq1[0]);
+      b_first_ready = false;
       dq[0] = first;
 #pragma unroll
       for (int a = 1; a <= kAhead; ++a) {
@@ -875,8 +897,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
   } else {
     round_bias(p, acc, wn0, g);
   }
-  if (p.y_vec == 2) {
-    // 16-byte aligned rows: the tile goes through LDS (the idle x ring, rows
+  if (kSwiglu || p.y_vec == 2) {
+    // 16-byte aligned rows (always so with the SwiGLU output): the tile goes through LDS (the idle x ring, rows
     // of 384 bytes, 16-byte chunks XOR-swizzled by row & 7) and leaves as
     // whole rows, so each 128-byte line of y is written by one request.
     static_assert(kBN * 2 == 384 && kBM * 384 <= kXD * kXBytes, "output staging fits the x ring");
@@ -893,18 +915,43 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(PrefillParams p) {
       }
     }
     __syncthreads();
+    if constexpr (kSwiglu) {
+      // Activation chunk q (8 columns) of a row: gate chunk q and up chunk
+      // q + 12 of the staged row, bf16(bf16(silu(g)) * u) as lf_swiglu.
 #pragma unroll
-    for (int r = 0; r < kBM * 24 / kThreads; ++r) {
-      const int id = tid + r * kThreads;
-      const int row = id / 24;
-      const int q = id - row * 24;
-      const int m = m0 + row;
-      const int n = n0 + q * 8;
-      if (m < p.m && n < p.n)
-        *reinterpret_cast<uint4*>(p.y + int64_t(m) * p.y_stride + n) =
-            *reinterpret_cast<const uint4*>(xring + row * 384 + ((q ^ (row & 7)) << 4));
+      for (int r = 0; r < kBM * 12 / kThreads; ++r) {
+        const int id = tid + r * kThreads;
+        const int row = id / 12;
+        const int q = id - row * 12;
+        const int m = m0 + row;
+        const int n = nt * (kBN / 2) + q * 8;
+        if (m < p.m && n < (p.n >> 1)) {
+          const uint4 gv = *reinterpret_cast<const uint4*>(xring + row * 384 + ((q ^ (row & 7)) << 4));
+          const uint4 uv = *reinterpret_cast<const uint4*>(xring + row * 384 + (((q + 12) ^ (row & 7)) << 4));
+          const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+          const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+          uint32_t o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = pack_bf16x2(silu_times(bf16_lo(gw[e]), bf16_lo(uw[e])),
+                               silu_times(bf16_hi(gw[e]), bf16_hi(uw[e])));
+          *reinterpret_cast<uint4*>(p.y + int64_t(m) * p.y_stride + n) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kBM * 24 / kThreads; ++r) {
+        const int id = tid + r * kThreads;
+        const int row = id / 24;
+        const int q = id - row * 24;
+        const int m = m0 + row;
+        const int n = n0 + q * 8;
+        if (m < p.m && n < p.n)
+          *reinterpret_cast<uint4*>(p.y + int64_t(m) * p.y_stride + n) =
+              *reinterpret_cast<const uint4*>(xring + row * 384 + ((q ^ (row & 7)) << 4));
+      }
     }
-  } else {
+  } else if constexpr (!kSwiglu) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int m = m0 + wm * 128 + i * 16 + c;
@@ -971,7 +1018,7 @@ int64_t prefill_workspace_bytes(int64_t m, int64_t n, int64_t k, int slices, int
 
 int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w,
                             const uint16_t* bias, const lf_lora* lora, uint16_t* y, int64_t y_stride,
-                            void* workspace, int64_t workspace_bytes, bool withhold, void* stream) {
+                            void* workspace, int64_t workspace_bytes, bool swiglu, bool withhold, void* stream) {
   const int slices = lora ? lora->num_slices : 1;
   const bool dq = w->scales == nullptr;
   const int64_t need = prefill_workspace_bytes(m, w->n, w->k, slices, lora ? lora->max_rank : 1);
@@ -1030,12 +1077,22 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
   p.withhold = withhold ? 1 : 0;
   p.spin_limit = withhold ? 64 : (1 << 20);
   p.mtiles = int((m + wide::kBM - 1) / wide::kBM);
-  const int64_t tiles = p.mtiles * ((w->n + wide::kBN - 1) / wide::kBN);
+  // SwiGLU output: each tile takes kBN / 2 activation columns (their gate and
+  // up rows) and stores 16-byte chunks of them.
+  LF_REQUIRE(!swiglu || p.y_vec == 2, "prefill SwiGLU output needs y 16-byte aligned with row stride %% 8 == 0");
+  const int64_t cols = swiglu ? w->n / 2 : w->n;
+  const int64_t bn = swiglu ? wide::kBN / 2 : wide::kBN;
+  const int64_t tiles = p.mtiles * ((cols + bn - 1) / bn);
   p.zparts = zparts_for(p.mtiles, tiles, device_cus());
   // LoRA launches put the z producers ahead of the GEMM tiles.
   const dim3 grid(unsigned(tiles + (lora ? p.mtiles * p.zparts : 0)));
-  if (lora) hipLaunchKernelGGL((wide::gemm_kernel<true>), grid, dim3(wide::kThreads), 0, s, p);
-  else hipLaunchKernelGGL((wide::gemm_kernel<false>), grid, dim3(wide::kThreads), 0, s, p);
+  if (swiglu) {
+    if (lora) hipLaunchKernelGGL((wide::gemm_kernel<true, true>), grid, dim3(wide::kThreads), 0, s, p);
+    else hipLaunchKernelGGL((wide::gemm_kernel<false, true>), grid, dim3(wide::kThreads), 0, s, p);
+  } else {
+    if (lora) hipLaunchKernelGGL((wide::gemm_kernel<true, false>), grid, dim3(wide::kThreads), 0, s, p);
+    else hipLaunchKernelGGL((wide::gemm_kernel<false, false>), grid, dim3(wide::kThreads), 0, s, p);
+  }
   LF_HIP(hipGetLastError());
   return kOk;
 }

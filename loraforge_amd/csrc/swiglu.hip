@@ -12,11 +12,6 @@ namespace {
 
 constexpr int kSwigluThreads = 256;
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  const float act = g / (1.0f + expf(-g));  // silu in fp32, as the reference's tl.exp form
-  const float a = bf16_to_f32(pack_bf16x2(act, 0.f) & 0xffffu);
-  return a * u;
-}
 
 // Eight outputs per thread: rows split into n / 8 chunks of 16 bytes.
 __global__ __launch_bounds__(kSwigluThreads) void swiglu_vec_kernel(const uint16_t* gu, int64_t rows, int64_t n,
@@ -35,7 +30,7 @@ __global__ __launch_bounds__(kSwigluThreads) void swiglu_vec_kernel(const uint16
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      o[k] = pack_bf16x2(silu_mul(bf16_lo(gw[k]), bf16_lo(uw[k])), silu_mul(bf16_hi(gw[k]), bf16_hi(uw[k])));
+      o[k] = pack_bf16x2(silu_times(bf16_lo(gw[k]), bf16_lo(uw[k])), silu_times(bf16_hi(gw[k]), bf16_hi(uw[k])));
     *reinterpret_cast<uint4*>(out + r * out_stride + c) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
@@ -50,7 +45,7 @@ __global__ __launch_bounds__(kSwigluThreads) void swiglu_scalar_kernel(const uin
     const int64_t c = i - r * n;
     const float g = bf16_to_f32(gu[r * in_stride + c]);
     const float u = bf16_to_f32(gu[r * in_stride + n + c]);
-    out[r * out_stride + c] = uint16_t(pack_bf16x2(silu_mul(g, u), 0.f) & 0xffffu);
+    out[r * out_stride + c] = uint16_t(pack_bf16x2(silu_times(g, u), 0.f) & 0xffffu);
   }
 }
 

@@ -293,9 +293,10 @@ def nf4_lora_linear(
     ``swiglu=True``: the weight is a merged gate/up projection (gate rows
     ``0 .. N/2``, up rows ``N/2 .. N``; with LoRA, slices ``[0, N/2, N]``) and
     the result is ``h = bf16(bf16(silu(gate)) * up)``, ``[..., N/2]``, of the
-    LoRA-updated bf16 gate and up outputs. Batches of up to 64 tokens compute
-    it in the decode kernels' epilogue (no gate/up round trip, no second
-    launch); larger ones run the linear and then ``silu_mul``.
+    LoRA-updated bf16 gate and up outputs, computed in the epilogue of the
+    decode kernels and of the prefill GEMM (no gate/up round trip, no second
+    launch); above 64 tokens into an ``out`` whose rows are not 16-byte
+    aligned, the linear and then ``silu_mul``.
 
     Above 64 tokens the library picks the prefill GEMM or the decode kernel
     over 64-token chunks (when the prefill tiles would leave most of the chip
@@ -336,9 +337,11 @@ def nf4_lora_linear(
         if lora is not None and lora.num_slices != 2:
             raise ValueError("SwiGLU output with LoRA needs the two gate/up slices")
         width = n // 2
-        # Batches above 64 tokens run the linear and then the activation (the
-        # activation is fused into the decode kernels' epilogue only).
-        if m > 64:
+        # The prefill GEMM stores the activation in 16-byte chunks: a caller's
+        # output whose rows are not 16-byte aligned takes the linear and then
+        # the activation above 64 tokens.
+        unaligned = out is not None and (out.data_ptr() % 16 or (out.dim() > 1 and out.stride(-2) % 8))
+        if m > 64 and unaligned:
             from .activation import silu_mul
 
             if out is not None:

@@ -110,5 +110,5 @@ def silu_mul(gate_bits, up_bits) -> np.ndarray:
     u = bf16_to_f32(up_bits)
     with np.errstate(over="ignore"):
         act = (g / (np.float32(1) + np.exp(-g, dtype=np.float32))).astype(np.float32)
-    act = bf16_to_f32(bf16_bits(act))
-    return bf16_bits((act * u).astype(np.float32))
+        act = bf16_to_f32(bf16_bits(act))
+        return bf16_bits((act * u).astype(np.float32))

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from loraforge_amd.ops import nf4_lora_linear
+from loraforge_amd.ops import LoraBatch, nf4_lora_linear, quantize_nf4
 from loraforge_amd.ops.activation import silu_mul
 from oracle import linear
 from oracle import nf4 as onf4
@@ -36,7 +36,11 @@ def assert_activation(actual_bits, expected_bits):
 def test_silu_mul_matches_oracle(rows, n, device):
     rng = np.random.default_rng(rows * 7 + n)
     vals = rng.standard_normal((rows, 2 * n)) * 3.0
-    vals[0, :6] = [0.0, -0.0, 40.0, -40.0, 88.0, -100.0]
+    # Zeros of both signs, around the overflow of e^-g (g near -88.7), past the exponent
+    # clamp of the activation (|g| >= 126) and huge gates.
+    vals[0, :8] = [0.0, -0.0, 40.0, -40.0, 88.0, -100.0, -88.5, -89.0]
+    if n >= 16:
+        vals[0, 8:16] = [126.0, 127.0, -126.5, -127.0, 1e30, -1e30, 3e38, -3e38]
     gu = _cases.bf16(vals)
     out = silu_mul(t16(gu, device))
     torch.cuda.synchronize()
@@ -165,6 +169,66 @@ def test_fused_swiglu_output_equals_the_separate_chain(m, with_lora, device):
     assert_activation(bits(h), linear.silu_mul(bits(gu)[:, :inter], bits(gu)[:, inter:]))
 
 
+@pytest.mark.parametrize("plan", ["prefill", "decode"])
+@pytest.mark.parametrize("m", [100, 300])
+def test_fused_swiglu_above_64_tokens_on_both_plans(m, plan, device):
+    """Above 64 tokens the activation is formed in the prefill GEMM's epilogue (each tile's
+    96 gate rows with the matching up rows; 1024 columns end in a partial tile) or in each
+    64-token decode chunk: the same bits as the linear on that plan followed by silu_mul."""
+    inter = 1024
+    case = _cases.fused_case(
+        m, 2 * inter, 512, ranks=(8, 16, 4), slices=2, bounds=[0, inter, 2 * inter], seed=980 + m, bias=True
+    )
+    x, q, st, lora, bias = to_device(case, device)
+    h = nf4_lora_linear(x, q, st, bias=bias, lora=lora, swiglu=True, plan=plan)
+    gu = nf4_lora_linear(x, q, st, bias=bias, lora=lora, plan=plan)
+    sep = silu_mul(gu)
+    base = nf4_lora_linear(x, q, st, bias=bias, swiglu=True, plan=plan)
+    base_sep = silu_mul(nf4_lora_linear(x, q, st, bias=bias, plan=plan))
+    # An output whose rows are not 16-byte aligned: the linear, then the activation.
+    backing = torch.zeros(m * inter + 1, dtype=torch.bfloat16, device=device)
+    odd = backing[1:].view(m, inter)
+    nf4_lora_linear(x, q, st, bias=bias, lora=lora, swiglu=True, plan=plan, out=odd)
+    torch.cuda.synchronize()
+    assert torch.equal(h, sep)
+    assert torch.equal(base, base_sep)
+    assert torch.equal(odd, sep)
+    if plan == "prefill":
+        close(bits(gu), _cases.fused_expected(case))
+
+
+def test_prefill_swiglu_c5_scale(device):
+    """The prefill GEMM with the activation in its epilogue at M = 2048 over c5's weight read as
+    a merged gate/up projection (N = 11008: 5504 activation columns, 58 column tiles, the last
+    partial), double quant, 8 segments of rank 32 over the gate/up slices: bit-identical to the
+    linear followed by silu_mul."""
+    m, inter, k, rank, segs = 2048, 5504, 4096, 32, 8
+    g = torch.Generator(device="cpu").manual_seed(736)
+    w = (torch.randn(2 * inter, k, generator=g) * 0.02).bfloat16().to(device)
+    q, st = quantize_nf4(w, compress_statistics=True)
+    del w
+    x = torch.randn(m, k, generator=g).bfloat16().to(device)
+    slots = torch.repeat_interleave(torch.arange(segs, dtype=torch.int32), m // segs).to(device)
+    i64 = dict(dtype=torch.int64, device=device)
+    n = 2 * inter
+    lora = LoraBatch(
+        (torch.randn(segs * 2 * rank * k, generator=g) * 0.02).bfloat16().to(device),
+        torch.arange(segs, **i64) * (2 * rank * k),
+        (torch.randn(segs * n * rank, generator=g) * 0.02).bfloat16().to(device),
+        torch.arange(segs, **i64) * (n * rank),
+        torch.full((segs,), rank, dtype=torch.int32, device=device),
+        torch.full((segs,), rank, dtype=torch.int32, device=device),
+        torch.full((segs,), 2.0, device=device),
+        slots,
+        torch.tensor([0, inter, n], dtype=torch.int32, device=device),
+        max_rank=rank,
+    )
+    h = nf4_lora_linear(x, q, st, lora=lora, swiglu=True, plan="prefill")
+    sep = silu_mul(nf4_lora_linear(x, q, st, lora=lora, plan="prefill"))
+    torch.cuda.synchronize()
+    assert torch.equal(h, sep)
+
+
 @pytest.mark.parametrize("m", [16, 48])
 def test_fused_swiglu_checks_out_like_the_linear(m, device):
     """swiglu=True checks out for every batch size the same way (device and storage of the
@@ -228,7 +292,7 @@ def test_fused_swiglu_graph_replay(device):
 @pytest.mark.parametrize("m", [33, 48, 64])
 def test_swiglu_flag_through_the_c_abi_at_32_row_groups(m, device):
     """LF_SWIGLU_OUTPUT at 33..64 tokens (32-row groups: gate tile and up tile meet in LDS),
-    which the Python wrapper leaves to the two-launch path, called through the C-ABI."""
+    called through the C-ABI."""
     from loraforge_amd import _lib
     from loraforge_amd.ops.fused import _lora_struct, _weight_struct
 
