@@ -25,7 +25,9 @@ benchmarks/check_qwen35_nf4_ops.py:11-41):
               the same update by lora_apply in one launch);
   c3          NF4 + double-quant SwiGLU MLP 4096 / 12288 (gate/up, SwiGLU,
               down), 16 rank-8 adapters, B = 1 / 8 / 64; c3_fused_* runs the
-              SwiGLU in the gate/up kernel's epilogue (two launches);
+              SwiGLU in the gate/up kernel's epilogue (two launches), c3_nested_*
+              the same with the kernels reading the double-quant state itself
+              (scales="nested") instead of cached fp32 scales;
   c4          NF4 4096^2, 256 tokens, 128 retained-rank adapters
               (ranks {4..64}), Zipf(1.1) routing;
   c5          prefill M = 2048, K = 4096, N = 11008, NF4 + double quant,
@@ -446,7 +448,13 @@ def c3_items(device, reps: int, copies: int = 6):
                 nf4_lora_linear(x, q1, s1, lora=l1, out=h, swiglu=True)
                 nf4_lora_linear(h, q2, s2, lora=l2, out=y)
 
-            return fn, fused
+            def nested():
+                # The same two launches reading the double-quant state itself (no
+                # fp32 scales resident; codes converted in LDS by each workgroup).
+                nf4_lora_linear(x, q1, s1, scales="nested", lora=l1, out=h, swiglu=True)
+                nf4_lora_linear(h, q2, s2, scales="nested", lora=l2, out=y)
+
+            return fn, fused, nested
 
         # Algorithmic bytes: packed weights, uint8 absmax codes, fp32 second-level
         # scales and code2 of both weights, the adapters used, and the activations
@@ -463,6 +471,9 @@ def c3_items(device, reps: int, copies: int = 6):
         meta[name] = dict(batch=batch, adapters_used=used, launches_per_call=3)
         items.append(Timed(f"c3_fused_b{batch}", [c[1] for c in chains], reps, work))
         meta[f"c3_fused_b{batch}"] = dict(batch=batch, adapters_used=used, launches_per_call=2, swiglu="gate/up epilogue")
+        items.append(Timed(f"c3_nested_b{batch}", [c[2] for c in chains], reps, work))
+        meta[f"c3_nested_b{batch}"] = dict(batch=batch, adapters_used=used, launches_per_call=2, swiglu="gate/up epilogue",
+                                           scales="nested state read in-kernel")
 
     for batch in (1, 8, 64):
         per_batch(batch)

@@ -142,9 +142,14 @@ int lf_row_expand_tiled(const uint16_t* z, const uint16_t* b, const int64_t* b_o
  * ------------------------------------------------------------------------ */
 typedef struct lf_nf4_weight {
   const uint8_t* qweight; /* [N*K/2] */
-  const float* scales;    /* fp32 [N*K/64], or NULL when double-quantised
-                             (prefill only: decode, M <= 64, takes fp32
-                             scales, e.g. from lf_nf4_prepare_scales_dq) */
+  const float* scales;    /* fp32 [N*K/64], or NULL when double-quantised:
+                             then the decode kernels stage the uint8 codes
+                             and absmax2 entries of their rows into LDS and
+                             convert them there (K % 256 == 0, dq_block a
+                             power of two >= 64, absmax_q 4-byte and code2
+                             16-byte aligned; other shapes, and the prefill
+                             GEMM, rebuild fp32 scales into the workspace
+                             first, as lf_nf4_prepare_scales_dq does) */
   const uint8_t* absmax_q;/* uint8 [N*K/64] (double quant) */
   const float* absmax2;   /* fp32 [ceil(N*K/64/dq_block)] */
   const float* code2;     /* fp32 [256] */
@@ -180,8 +185,12 @@ typedef struct lf_lora {
  * status word and the shrink partials, each tagged with the call that wrote
  * it); it must be zero before the first call and is never reset between
  * calls. A prefill call uses the rest for its z rows and, for a double-quant
- * weight, the rebuilt fp32 block scales. Decode and prefill calls may share
- * one workspace; calls that share one workspace must not overlap in time. */
+ * weight, the rebuilt fp32 block scales; a decode call of a double-quant
+ * weight whose kernel does not read the nested state itself rebuilds them
+ * after the prefill's flag region (a decode call with fp32 scales, or whose
+ * kernel reads the nested state, needs only the header). Decode and prefill
+ * calls may share one workspace; calls that share one workspace must not
+ * overlap in time. */
 int64_t lf_nf4_lora_workspace_size(int64_t m, int64_t n, int64_t k, int32_t num_slices, int32_t max_rank);
 
 /* x [m, K] bf16 with row stride x_stride (multiple of 8, 16-byte aligned);

@@ -9,6 +9,7 @@
 #include <type_traits>
 
 #include "call_epoch.h"
+#include "dq_scales.h"
 #include "lds_pipeline.h"
 #include "nf4_common.h"
 #include "../../include/loraforge_amd.h"
@@ -42,6 +43,15 @@ struct GemvParams {
   int gated_half;  // SwiGLU output: n / 2 (a group's rows: R / 2 gate rows and the matching up rows), else 0
   int sc_stride;  // floats per row of a wave's scale area (narrow kScPre tiles: odd; wide: a power of two)
   int sc_bytes;   // bytes of a wave's scale area in dynamic LDS (multiple of 256)
+  uint32_t sc_magic;  // ceil(2^32 / sc_stride): pos / sc_stride as a high multiply (pos < 2^16; stride > 1)
+  // Double-quant block scales (absmax_q non-null, scales null): each base wave
+  // stages them into its scale area and converts them there (dq_scales.h).
+  const uint8_t* absmax_q;
+  const float* absmax2;
+  const float* code2;
+  const float* dq_offset;
+  int dq_shift;   // log2(dq_block)
+  int a2_len;     // entries of absmax2
   // LoRA (kLora variants only).
   const uint16_t* a_store;
   const int64_t* a_offsets;
@@ -782,6 +792,54 @@ GemvPlan gemv_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
 
 // The LoRA fields of the launch parameters (workspace control header, tagged
 // partials and the unit plan), shared by both decode launchers.
+// Block scales of a decode launch. fp32 scales are streamed as given. A
+// nested state is read by the kernel itself (dq_scales.h) where the layout
+// allows it: the codes' rows start on dwords (K % 256 == 0, the code pointer
+// 4-byte aligned), dq_block is a power of two of at least 64, code2 16-byte aligned, a row
+// half of `rows` rows spans at most 32 absmax2 entries, and the wave's
+// staging fits its scale area (stage_fits). Otherwise the fp32 scales are
+// rebuilt into the workspace (after the prefill's flag region, which holds
+// only tags) by lf_nf4_prepare_scales_dq first.
+inline int64_t decode_scales_offset() { return kWorkspaceHeader + kFlagRegion; }
+inline int64_t decode_scales_bytes(int64_t n, int64_t k) { return (n * (k / 64) * 4 + 255) / 256 * 256; }
+
+inline bool dq_layout_ok(const lf_nf4_weight* w, int rows) {
+  if (w->scales || !w->absmax_q || !w->absmax2 || !w->code2 || !w->offset) return false;
+  const int64_t nblk = w->k / 64, dq = w->dq_block;
+  return w->k % 256 == 0 && (reinterpret_cast<uintptr_t>(w->absmax_q) & 3u) == 0 && aligned16(w->code2) && dq >= 64 &&
+         (dq & (dq - 1)) == 0 && dq < (int64_t(1) << 30) && int64_t(rows / 2) * nblk / dq + 2 <= 32;
+}
+
+inline void fill_dq_params(GemvParams& p, const lf_nf4_weight* w) {
+  p.absmax_q = w->absmax_q;
+  p.absmax2 = w->absmax2;
+  p.code2 = w->code2;
+  p.dq_offset = w->offset;
+  p.dq_shift = __builtin_ctzll(uint64_t(w->dq_block));
+  const int64_t blocks = w->n * (w->k / 64);
+  p.a2_len = int((blocks + w->dq_block - 1) / w->dq_block);
+}
+
+// (Stride 1 has no 32-bit magic: the kernels take pos itself.)
+inline uint32_t stride_magic(int stride) {
+  return stride <= 1 ? 0u : uint32_t(((uint64_t(1) << 32) + uint64_t(stride) - 1) / uint64_t(stride));
+}
+
+// fp32 scales of a nested state rebuilt into the workspace (the decode
+// kernels' fallback).
+inline int rebuild_scales(const lf_nf4_weight* w, void* workspace, int64_t workspace_bytes, void* stream,
+                          const float** scales) {
+  const int64_t need = decode_scales_offset() + decode_scales_bytes(w->n, w->k);
+  LF_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
+             "workspace too small for the rebuilt scales: need %lld bytes", (long long)need);
+  float* out = reinterpret_cast<float*>(static_cast<char*>(workspace) + decode_scales_offset());
+  const int rc = lf_nf4_prepare_scales_dq(w->absmax_q, w->absmax2, w->code2, w->offset, w->dq_block, out,
+                                          w->n * (w->k / 64), stream);
+  if (rc != kOk) return rc;
+  *scales = out;
+  return kOk;
+}
+
 inline int fill_lora_params(GemvParams& p, const GemvPlan& pl, const lf_lora* lora, int64_t m, void* workspace,
                             int64_t workspace_bytes, bool withhold) {
   LF_REQUIRE(workspace && workspace_bytes >= kWorkspaceHeader, "workspace too small: need %lld bytes",

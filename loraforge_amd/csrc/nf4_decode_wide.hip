@@ -584,6 +584,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   __shared__ __attribute__((aligned(16))) char lora_lds[kLora ? WL::kBytes : 16];
   __shared__ int prod_done;   // base waves that have written their first-unit partials
   __shared__ int table_done;  // (LoRA) base waves 0..3 that have written their part of the decode table
+  __shared__ int dq_ready;    // double quant: wave 0's code2 copies have landed
   extern __shared__ __attribute__((aligned(16))) char scale_lds[];  // kBase * p.sc_bytes (+16)
 
   const int xcc = blockIdx.x & 7;
@@ -605,6 +606,9 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   char* myw = wring + (base ? wave : 0) * kDWG * kWGroup;
   char* myx = xring + (base ? wave : 0) * kDX * kXSlot;
   char* mysc = scale_lds + (base ? wave : 0) * p.sc_bytes;
+  // Double quant: code2 after the scale areas (1 KiB of dynamic LDS that only
+  // those launches allocate).
+  float* dq_table = reinterpret_cast<float*>(scale_lds + kBase * p.sc_bytes + 16);
   float* red = reinterpret_cast<float*>(lora_lds + WL::kZ);  // first-unit partials (before z is gathered there)
 
   // Copy addresses: a uniform base (scalar registers) plus a 32-bit per-lane
@@ -678,6 +682,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
         reinterpret_cast<TileMeta*>(lora_lds + WL::kMeta)->ready = 0;
         prod_done = 0;
         table_done = 0;
+        dq_ready = 0;
       }
       epoch = __hip_atomic_load(p.ce.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       g_tile = p.token_slots[t0 + min(lane, mt - 1)];
@@ -696,9 +701,21 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   bool has0 = false;
   bool single = false;  // the first unit is contracted inside the loop (from pre4)
   UnitPieces<4> pre4;
+  // Double quant: the codes and absmax2 entries are staged instead of fp32
+  // scales (code2 requested ahead of every copy) and converted before the loop.
+  const bool dq = !kResidual && p.absmax_q != nullptr;
+  float dq_off = 0.f;
+  DqStage dqs{};
   if (base) {
+    if (wave == 0 && dq) dq_issue_code2(p, dq_table, lane);  // ahead of wave 0's staging
     if (nb > 0) {
-      issue_scales(p, mysc, lo, hi, kb0, nb, lane);
+      if (dq) {
+        dq_off = sload(p.dq_offset, 0);
+        dqs = dq_stage(p, p.sc_bytes, kRows, lo, hi, kb0, nb);
+        dq_issue(p, mysc, dqs, kRows, lo, hi, kb0, lane);
+      } else {
+        issue_scales(p, mysc, lo, hi, kb0, nb, lane);
+      }
 #pragma unroll
       for (int g2 = 0; g2 < kDWG; ++g2)
         if (g2 < groups) issue_w(g2, g2);
@@ -755,6 +772,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
     if (threadIdx.x == 0) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) table[i] = cb[i];
+      dq_ready = 0;  // set by wave 0 after the barriers below
     }
     if constexpr (!kExact) {
       lds_barrier();
@@ -789,6 +807,31 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
       if (single) contract = true;
       else unit_contract(p, un0, red, &prod_done, wave, lane);
     }
+  }
+
+  if (dq) {
+    // The staging (and wave 0's code2 copies before it) was requested first:
+    // it has landed once no more than the weight groups and x blocks
+    // requested after it are outstanding (loads complete in issue order; a
+    // producer's unit pieces came later still). Wave 0 raises dq_ready
+    // whether or not it has blocks (short K); the others wait for it, with
+    // a bound, before reading code2.
+    const int after = nb > 0 ? 4 * (min(kDWG, groups) + min(kDX, nb)) : 0;
+    switch (after) {
+      case 16: wait_vm<16>(); break;
+      case 12: wait_vm<12>(); break;
+      case 8: wait_vm<8>(); break;
+      default: wait_vm<0>(); break;
+    }
+    if (wave == 0) {
+      if (lane == 0) __hip_atomic_store(&dq_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else if (nb > 0) {
+      for (int spins = 0; spins < kSpinLimit &&
+                          *(const volatile __attribute__((address_space(3))) int*)(&dq_ready) == 0;
+           ++spins)
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (nb > 0) dq_convert<kDqEntries>(p, mysc, dqs, kRows, lo, hi, kb0, nb, dq_table, dq_off, lane);
   }
 
   f32x16 acc;
@@ -980,6 +1023,18 @@ int64_t scale_area_bytes(int64_t nblk) { return (kRows * scale_stride(nblk) * 4 
 
 }  // namespace
 
+// Whether the wide kernel reads this nested state itself (dq_scales.h).
+// (The code2 table's 1 KiB must fit beside the largest static LDS, that of
+// the LoRA variant with one weight group per wave.)
+bool wide_takes_dq(const lf_nf4_weight* w) {
+  const int64_t nblk = w->k / 64;
+  const int64_t nbw = (nblk + kBase - 1) / kBase;
+  const int64_t smallest = int64_t(kBase) * (kWGroup + kDX * kXSlot) + 256 * 16 * 4 + 64 + WL::kBytes;
+  return dq_layout_ok(w, kRows) && dq_cols_per_lane(kRows, int(scale_stride(nblk))) <= kDqEntries &&
+         dq_stage_bytes(kRows, int(nbw)) <= scale_area_bytes(nblk) &&
+         smallest + kBase * scale_area_bytes(nblk) + 16 + 1024 <= kLdsBytes;
+}
+
 int device_cus();
 
 // Shrink units of the wide kernel: k-slices only as many as keep a tile's
@@ -1063,7 +1118,7 @@ int launch_lora_apply_wide(const uint16_t* x, int64_t m, int64_t x_stride, int64
 int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                        const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
                        bool exact, bool swiglu, bool withhold, void* stream) {
-  LF_REQUIRE(decode_wide_fits(m, w->n, w->k, lora) && w->scales != nullptr, "wide decode: call outside its range");
+  LF_REQUIRE(decode_wide_fits(m, w->n, w->k, lora), "wide decode: call outside its range");
   LF_REQUIRE(!swiglu || w->n % 64 == 0, "SwiGLU output needs N a multiple of 64");
   GemvParams p{};
   p.x = x;
@@ -1083,12 +1138,24 @@ int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_
   const int64_t nblk = w->k / 64;
   p.sc_stride = int(scale_stride(nblk));
   p.sc_bytes = int(scale_area_bytes(nblk));
+  p.sc_magic = stride_magic(p.sc_stride);
+  if (!w->scales) {
+    // A nested state: staged and converted by the kernel where its layout
+    // allows (a wave's area rows x stride at most 16 entries per lane),
+    // else fp32 scales rebuilt into the workspace.
+    if (wide_takes_dq(w)) {
+      fill_dq_params(p, w);
+    } else {
+      const int rc = rebuild_scales(w, workspace, workspace_bytes, stream, &p.scales);
+      if (rc != kOk) return rc;
+    }
+  }
   if (lora) {
     const GemvPlan pl = wide_plan(m, w->n, w->k, device_cus(), lora->num_slices * lora->max_rank);
     const int rc = fill_lora_params(p, pl, lora, m, workspace, workspace_bytes, withhold);
     if (rc != kOk) return rc;
   }
-  const int64_t dyn = int64_t(kBase) * p.sc_bytes + 16;
+  const int64_t dyn = int64_t(kBase) * p.sc_bytes + 16 + (p.absmax_q ? 1024 : 0);
   const int64_t octets = (p.row_groups + 7) / 8;
   const int64_t grid = octets * 8 * p.tiles;
   LF_REQUIRE(grid < (int64_t(1) << 31), "wide decode: grid too large");

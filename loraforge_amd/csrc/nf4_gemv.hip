@@ -412,6 +412,11 @@ __device__ __forceinline__ void issue_scales(const GemvParams& p, char* area, in
 template <int RT, int XR>
 constexpr int kMinWavesPerSimd = (RT == 1 && XR <= 8) ? 4 : 2;
 
+// Double quant: columns of its row a lane converts, at most (16-row groups
+// take four lanes a row, 32-row groups two).
+template <int RT>
+constexpr int kDqCols = RT == 1 ? 8 : 16;
+
 template <int RT, int XR, bool kExact, bool kLora, bool kResidual, bool kSP>
 __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv_kernel(GemvParams p) {
   using TL = Tile<RT, XR, kSP>;
@@ -426,6 +431,7 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   __shared__ float red[kLora ? kProd * 192 : 1];
   __shared__ int prod_done;  // contraction waves that have written their first-unit partials
   __shared__ f32x4 up_vals[RT == 2 ? TL::kTT * 64 : 1];  // SwiGLU output: the up tile's final values
+  __shared__ int dq_ready;  // double quant: wave 0's code2 copies have landed
   extern __shared__ __attribute__((aligned(16))) char scale_lds[];  // kScPre: kBase * p.sc_bytes (+16)
 
   const int rg = blockIdx.x % p.row_groups;
@@ -444,6 +450,12 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   const int nst = kResidual ? 0 : (kend - kb0 + TL::kSB - 1) / TL::kSB;
   char* myring = ring + wave * D * TL::kStage;  // waves below kBase only
   char* myscales = scale_lds + wave * p.sc_bytes;  // kScPre, waves below kBase only
+  // Double quant (kScPre): code2 after the scale areas (1 KiB of dynamic LDS
+  // that only those launches allocate).
+  float* dq_table = reinterpret_cast<float*>(scale_lds + kBase * p.sc_bytes + 16);
+  const bool dq = TL::kScPre && !kResidual && p.absmax_q != nullptr;
+  float dq_off = 0.f;
+  DqStage dqs{};
   static_assert(!kResidual || (kLora && !kExact), "the residual form is a LoRA-only variant");
 
   // Codebook (and the LoRA slice bounds) through scalar loads: no vector
@@ -477,7 +489,18 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
     auto stage_kb = [&](int s) { return min(kb0 + s * TL::kSB, nblk - 1); };
     // kScPre: the wave's scales first (the wait for its first stage covers
     // them, and the unit's fragments are not queued behind them for long).
-    if constexpr (TL::kScPre && !kResidual) issue_scales<TL>(p, myscales, lo, hi, kb0, kend - kb0, lane);
+    if constexpr (TL::kScPre && !kResidual) {
+      if (dq) {
+        // Double quant: code2 (wave 0, ahead of everything), then the
+        // wave's codes and absmax2 entries instead of fp32 scales.
+        if (wave == 0) dq_issue_code2(p, dq_table, lane);
+        dq_off = sload(p.dq_offset, 0);
+        dqs = dq_stage(p, p.sc_bytes, TL::kR, lo, hi, kb0, kend - kb0);
+        dq_issue(p, myscales, dqs, TL::kR, lo, hi, kb0, lane);
+      } else {
+        issue_scales<TL>(p, myscales, lo, hi, kb0, kend - kb0, lane);
+      }
+    }
     if constexpr (kLora) {
       has0 = int(blockIdx.x) < p.producers && int(blockIdx.x) < p.units && unit_of(p, blockIdx.x, un0);
       if (has0) first_frags<kFirst, kProd>(p, un0, wave, lane, pre);
@@ -533,6 +556,7 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
   if (threadIdx.x == 0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) table[i] = cb[i];
+    dq_ready = 0;  // set by wave 0 after the barrier below
     if constexpr (kLora) {
       reinterpret_cast<TileMeta*>(lora_lds + LoraLds<TL>::kMeta)->ready = 0;
       prod_done = 0;
@@ -588,6 +612,22 @@ __global__ __launch_bounds__(kThreads, (kMinWavesPerSimd<RT, XR>)) void nf4_gemv
       wait_vm<kResidual ? 0 : D * TL::kDma>();
       first_unit_partials<kFirst, kProd>(p, un0, pre, red, &prod_done, wave, lane);
     }
+  }
+  if (dq && wave < kBase) {
+    // The staging (and wave 0's code2 copies) came before the unit's
+    // fragments and the D stages: it has landed once only the stages are
+    // outstanding. Wave 0 then raises dq_ready; the others wait for it, with
+    // a bound, before reading code2.
+    wait_vm<D * TL::kDma>();
+    if (wave == 0) {
+      if (lane == 0) __hip_atomic_store(&dq_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+      for (int spins = 0; spins < kSpinLimit &&
+                          *(const volatile __attribute__((address_space(3))) int*)(&dq_ready) == 0;
+           ++spins)
+        __builtin_amdgcn_s_sleep(1);
+    }
+    dq_convert<kDqCols<RT>>(p, myscales, dqs, TL::kR, lo, hi, kb0, kend - kb0, dq_table, dq_off, lane);
   }
   // Scales of stage s: kScPre tiles read the wave's scale area (block
   // kb0 + s kSB onwards), the others the stage's slot.
@@ -769,18 +809,47 @@ template <int RT, int XR, bool kExact, bool kLora>
 int launch_scaled(dim3 grid, hipStream_t s, GemvParams p) {
   constexpr int kBase = kLora ? kWaves - 1 : kWaves;
   const ScaleArea a = scale_area(p.k >> 6, kBase, 16 * RT);
-  const int64_t dyn = int64_t(kBase) * a.bytes + 16;
+  // Double quant: each area grows by the staging of the codes (past its fp32
+  // entries), and the code2 table follows the areas.
+  const int nbw = ((p.k >> 6) + kBase - 1) / kBase;
+  const int area = a.bytes + (p.absmax_q ? dq_stage_bytes(16 * RT, nbw) : 0);
+  const int64_t dyn = int64_t(kBase) * area + 16 + (p.absmax_q ? 1024 : 0);
   static int64_t static_lds = -1;
   auto fn = nf4_gemv_kernel<RT, XR, kExact, kLora, false, true>;
   const int64_t st = static_lds_of(fn, static_lds);
   if (st >= 0 && st + dyn <= kLdsBytes) {
     p.sc_stride = a.stride;
-    p.sc_bytes = a.bytes;
+    p.sc_bytes = area;
+    p.sc_magic = stride_magic(a.stride);
     hipLaunchKernelGGL(fn, grid, dim3(kThreads), size_t(dyn), s, p);
   } else {
+    // (A nested state is only passed where the variant above fits.)
+    LF_REQUIRE(p.absmax_q == nullptr, "decode: double-quant scales need the scales-in-LDS variant");
     hipLaunchKernelGGL((nf4_gemv_kernel<RT, XR, kExact, kLora, false, false>), grid, dim3(kThreads), 0, s, p);
   }
   return kOk;
+}
+
+// Whether the scales-in-LDS variant of a tile reads a nested state itself
+// (dq_scales.h): the layout conditions, and the variant with its areas grown
+// by the staging and the code2 table fitting LDS.
+template <int RT, int XR, bool kExact, bool kLora>
+bool dq_variant_ok(const lf_nf4_weight* w) {
+  constexpr int kBase = kLora ? kWaves - 1 : kWaves;
+  constexpr int kRows = 16 * RT;
+  const int nblk = int(w->k >> 6);
+  const ScaleArea a = scale_area(nblk, kBase, kRows);
+  const int nbw = (nblk + kBase - 1) / kBase;
+  if (!dq_layout_ok(w, kRows) || dq_cols_per_lane(kRows, a.stride) > kDqCols<RT>) return false;
+  static int64_t static_lds = -1;
+  const int64_t st = static_lds_of(nf4_gemv_kernel<RT, XR, kExact, kLora, false, true>, static_lds);
+  return st >= 0 && st + int64_t(kBase) * (a.bytes + dq_stage_bytes(kRows, nbw)) + 16 + 1024 <= kLdsBytes;
+}
+
+template <int RT, int XR>
+bool dq_tile_ok(const lf_nf4_weight* w, bool lora, bool exact) {
+  if (lora) return exact ? dq_variant_ok<RT, XR, true, true>(w) : dq_variant_ok<RT, XR, false, true>(w);
+  return exact ? dq_variant_ok<RT, XR, true, false>(w) : dq_variant_ok<RT, XR, false, false>(w);
 }
 
 template <int RT, int XR>
@@ -808,7 +877,27 @@ int device_cus() {
   return cached[dev];
 }
 
-int64_t gemv_workspace_bytes(int64_t, int64_t, int64_t, int, int) { return kWorkspaceHeader; }
+// The control header with the tagged partials, then (after the prefill's flag
+// region) room for fp32 scales rebuilt from a nested state.
+int64_t gemv_workspace_bytes(int64_t, int64_t n, int64_t k, int, int) {
+  return decode_scales_offset() + decode_scales_bytes(n, k);
+}
+
+int rebuild_decode_scales(const lf_nf4_weight* w, void* workspace, int64_t workspace_bytes, void* stream,
+                          const float** scales) {
+  return rebuild_scales(w, workspace, workspace_bytes, stream, scales);
+}
+
+// Whether the narrow kernel reads this nested state itself (the tile that
+// launch_nf4_gemv picks for m tokens).
+bool gemv_takes_dq(int64_t m, const lf_nf4_weight* w, const lf_lora* lora, bool exact) {
+  const bool lo = lora != nullptr;
+  if (m <= 2) return dq_tile_ok<1, 2>(w, lo, exact);
+  if (m <= 8) return dq_tile_ok<1, 8>(w, lo, exact);
+  if (m <= 16) return dq_tile_ok<1, 16>(w, lo, exact);
+  if (m <= 32) return dq_tile_ok<1, 32>(w, lo, exact);
+  return dq_tile_ok<2, 32>(w, lo, exact);
+}
 
 // Fused NF4 + multi-LoRA linear for 1..64 tokens with fp32 block scales.
 // residual: no weight (only w->n and w->k are read) and a LoRA batch: y is
@@ -817,7 +906,14 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
                     const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
                     bool exact, bool swiglu, bool withhold, void* stream, bool residual) {
   LF_REQUIRE(m >= 1 && m <= 64, "decode path handles 1..64 tokens");
-  LF_REQUIRE(residual || w->scales != nullptr, "decode takes fp32 block scales (prepare double-quant scales first)");
+  // A nested state: read by the kernel where its scales-in-LDS variant takes
+  // it, else fp32 scales rebuilt into the workspace.
+  const float* scales = w->scales;
+  const bool dq_in = !residual && !scales && gemv_takes_dq(m, w, lora, exact);
+  if (!residual && !scales && !dq_in) {
+    const int rc = rebuild_scales(w, workspace, workspace_bytes, stream, &scales);
+    if (rc != kOk) return rc;
+  }
   LF_REQUIRE(!residual || (lora && !bias && !swiglu && !exact), "the residual form takes a LoRA batch and nothing else");
   const GemvPlan pl = gemv_plan(m, w->n, w->k, device_cus(), lora ? lora->num_slices * lora->max_rank : 1);
   LF_REQUIRE(w->n % pl.rows == 0, "output width must be a multiple of %d", pl.rows);
@@ -826,7 +922,7 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   p.x_stride = x_stride;
   p.m = int(m);
   p.q = w->qweight;
-  p.scales = w->scales;
+  p.scales = scales;
   p.code = w->code;
   p.n = int(w->n);
   p.k = int(w->k);
@@ -835,6 +931,7 @@ int launch_nf4_gemv(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4
   p.y_stride = y_stride;
   p.row_groups = pl.row_groups;
   p.gated_half = swiglu ? int(w->n / 2) : 0;  // n % 32 == 0: R / 2 divides n / 2
+  if (dq_in) fill_dq_params(p, w);
   if (lora) {
     const int rc = fill_lora_params(p, pl, lora, m, workspace, workspace_bytes, withhold);
     if (rc != kOk) return rc;

@@ -18,6 +18,10 @@ int launch_nf4_lora_prefill(const uint16_t* x, int64_t m, int64_t x_stride, cons
                             void* workspace, int64_t workspace_bytes, bool swiglu, bool withhold, void* stream);
 int device_cus();
 bool decode_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora);
+bool wide_takes_dq(const lf_nf4_weight* w);
+bool gemv_takes_dq(int64_t m, const lf_nf4_weight* w, const lf_lora* lora, bool exact);
+int rebuild_decode_scales(const lf_nf4_weight* w, void* workspace, int64_t workspace_bytes, void* stream,
+                          const float** scales);
 bool lora_apply_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora);
 int launch_lora_apply_wide(const uint16_t* x, int64_t m, int64_t x_stride, int64_t n, int64_t k, const lf_lora* lora,
                            uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes, bool withhold,
@@ -118,31 +122,36 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
   // Above 32 tokens: the wide decode kernel (one launch, base linear with or
   // without LoRA and the SwiGLU output), unless the prefill GEMM is forced or
   // cheaper, or the shape is outside the kernel's range.
-  if (m > 32 && w->scales && lf::decode_wide_fits(m, n, k, lora) && !(flags & LF_PLAN_PREFILL) &&
+  if (m > 32 && lf::decode_wide_fits(m, n, k, lora) && !(flags & LF_PLAN_PREFILL) &&
       (m <= lf::kDecodeMaxTokens || (flags & LF_PLAN_DECODE_CHUNKS) || lf::wide_cheaper(m, n, k)))
     return lf::launch_decode_wide(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact,
                                   swiglu, withhold, stream);
-  if (m <= lf::kDecodeMaxTokens) {
-    // The decode kernel streams fp32 block scales (as the reference serves
-    // decode from prepare_scales output): nested states go through
-    // lf_nf4_prepare_scales_dq once per weight.
-    LF_REQUIRE(w->scales != nullptr,
-               "decode (M <= 64) takes fp32 block scales: build them with lf_nf4_prepare_scales_dq");
+  if (m <= lf::kDecodeMaxTokens)
     return lf::launch_decode(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
                              withhold, stream);
-  }
   bool chunked = false;
-  if (flags & LF_PLAN_DECODE_CHUNKS) {
-    LF_REQUIRE(w->scales != nullptr, "the chunked decode plan takes fp32 block scales");
-    chunked = true;
-  } else if (!(flags & LF_PLAN_PREFILL)) {
-    chunked = w->scales != nullptr && lf::decode_chunks_cheaper(m, n, k, lora != nullptr);
-  }
+  if (flags & LF_PLAN_DECODE_CHUNKS) chunked = true;
+  else if (!(flags & LF_PLAN_PREFILL)) chunked = lf::decode_chunks_cheaper(m, n, k, lora != nullptr);
   if (!chunked)
     return lf::launch_nf4_lora_prefill(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes,
                                        swiglu, withhold, stream);
   // 64-token chunks in token order on the caller's stream; each is one decode
-  // launch over its rows of x, y and the token routes.
+  // launch over its rows of x, y and the token routes. A nested state that a
+  // chunk's kernel does not read itself is rebuilt to fp32 scales once, ahead
+  // of the chunks.
+  lf_nf4_weight wc = *w;
+  if (!w->scales) {
+    const int64_t last = m - (m - 1) / lf::kDecodeMaxTokens * lf::kDecodeMaxTokens;
+    auto reads = [&](int64_t mc) {
+      return (mc > 32 && lf::decode_wide_fits(mc, n, k, lora)) ? lf::wide_takes_dq(w)
+                                                               : lf::gemv_takes_dq(mc, w, lora, exact);
+    };
+    if (!reads(lf::kDecodeMaxTokens) || !reads(last)) {
+      const int rc = lf::rebuild_decode_scales(w, workspace, workspace_bytes, stream, &wc.scales);
+      if (rc != lf::kOk) return rc;
+    }
+  }
+  w = &wc;
   for (int64_t t0 = 0; t0 < m; t0 += lf::kDecodeMaxTokens) {
     const int64_t mc = std::min<int64_t>(lf::kDecodeMaxTokens, m - t0);
     lf_lora part{};

@@ -17,6 +17,7 @@
 // wrote them, arrival counters return to zero at the end of every call).
 // Every call on a device shares that device's array and leaves its contents
 // behind: calls that overlap in time on one GPU race.
+#include <algorithm>
 #include <mutex>
 
 #include "nf4_common.h"
@@ -74,9 +75,13 @@ extern "C" int lf_nf4_lora_linear_noalloc(const uint16_t* x, int64_t m, int64_t 
   LF_REQUIRE(w != nullptr, "weight descriptor required");
   LF_REQUIRE(m >= 0, "token count out of range");
   if (m == 0) return lf::kOk;
-  const int64_t need =
+  int64_t need =
       lf_nf4_lora_workspace_size(m, w->n, w->k, lora ? lora->num_slices : 1, lora ? lora->max_rank : 1);
   LF_REQUIRE(need >= 0, "invalid problem size");
+  // A decode call with fp32 scales uses only the control header (the size
+  // above also covers fp32 scales rebuilt from a nested state, which the
+  // launch then checks against the scratch itself).
+  if (w->scales && m <= 64) need = std::min<int64_t>(need, lf::kWorkspaceHeader);
   LF_REQUIRE(need <= lf::kScratchBytes,
              "problem needs %lld bytes of workspace; the allocation-free entry point holds %lld (use "
              "lf_nf4_lora_linear with a caller workspace)",

@@ -127,14 +127,16 @@ def _workspace(device, stream: int, size: int, kind: str = "fused"):
 
 
 def _kernel_takes_nested(m: int, exact: bool, plan: str | None = None) -> bool:
-    """Whether the call for ``m`` tokens passes a nested state to the library.
+    """Whether a call for ``m`` tokens with ``scales=None`` passes a nested state to the library.
 
-    The decode kernel streams fp32 block scales, so decode calls (and the
-    chunked decode plan) take the prepared scales, rebuilt once per weight
-    and cached on the state. The prefill launch rebuilds them itself into its
-    workspace on every call; by default calls above 64 tokens also take the
-    cached scales (no per-call rebuild), and ``exact=True`` passes the nested
-    state, which keeps them on the prefill GEMM's exact weights.
+    Decode calls (and the chunked decode plan) take the prepared scales,
+    rebuilt once per weight and cached on the state: the decode kernels can
+    read the nested state themselves (``scales="nested"``), but converting it
+    costs each workgroup about 1.3 us before its weight loop, more than the
+    3 bytes per 64 weights it saves. The prefill launch rebuilds fp32 scales
+    into its workspace on every call; by default calls above 64 tokens also
+    take the cached scales (no per-call rebuild), and ``exact=True`` passes
+    the nested state, which keeps them on the prefill GEMM's exact weights.
     """
     return m > 64 and exact and plan != "decode"
 
@@ -191,7 +193,11 @@ def _weight_struct(qweight, state, scales, n, k, device, m=0, exact=False, plan=
     keep = [qweight, code]
     if scales is None and not state.nested:
         scales = state.absmax
-    if scales is None and not _kernel_takes_nested(m, exact, plan):
+    if isinstance(scales, str):
+        if scales != "nested" or not state.nested:
+            raise ValueError('scales="nested" needs a double-quant (nested) state')
+        scales = None
+    elif scales is None and not _kernel_takes_nested(m, exact, plan):
         scales = _prepared_scales(qweight, state)
     if scales is not None:
         vector(scales.reshape(-1), "scales", torch.float32, device, n * k // 64)
@@ -279,8 +285,13 @@ def nf4_lora_linear(
     x: bf16 ``[..., K]`` with unit column stride. qweight: packed uint8
     ``N*K/2`` (high nibble first). state: NF4 state (``NF4State`` or a
     bitsandbytes ``QuantState``); ``scales`` (fp32 ``N*K/64``, e.g. from
-    ``prepare_scales``) overrides its absmax, otherwise nested states are
-    reconstructed inside the kernel. Returns bf16 ``[..., N]`` (``out`` if given).
+    ``prepare_scales``) overrides its absmax. For a nested (double-quant)
+    state, ``scales=None`` uses fp32 scales prepared once per weight and
+    cached on the state (the faster decode), and ``scales="nested"`` hands
+    the library the nested state itself: the decode kernels stage the uint8
+    codes into LDS and convert them there (no fp32 scales resident, 1 byte
+    per 64 weights read instead of 4, about 1.3 us more per workgroup), and
+    the prefill GEMM rebuilds fp32 scales into its workspace per call. Returns bf16 ``[..., N]`` (``out`` if given).
     Launches on the current stream; the workspace (cached per device and
     stream unless passed) must not be shared by overlapping calls.
 
