@@ -573,9 +573,12 @@ __device__ __forceinline__ void lora_wave(const GemvParams& p, char* lora_lds, f
 // octets, so every workgroup of the grid is a real one and counts in once).
 // kResidual (with kLora): no weight; y is the base and is updated in place
 // with each routed token's LoRA delta (the one-launch shrink + expand).
-template <bool kExact, int kDWG, bool kLora, bool kResidual = false>
+// kDq: the launch passes a double-quant state (dq_scales.h), a variant of
+// its own so that the fp32-scale kernels carry none of its registers.
+template <bool kExact, int kDWG, bool kLora, bool kResidual = false, bool kDq = false>
 __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_wide_kernel(GemvParams p) {
   static_assert(!kResidual || (kLora && !kExact), "the residual form is a LoRA-only variant");
+  static_assert(!(kResidual && kDq), "the residual form reads no weight");
   constexpr int kCP = kLora ? 8 : 16;  // pair-table copies (lane l reads copy l % kCP); 8 leave LDS for LoRA
   __shared__ __attribute__((aligned(16))) char wring[kBase * kDWG * kWGroup];
   __shared__ __attribute__((aligned(16))) char xring[kBase * kDX * kXSlot];
@@ -703,13 +706,15 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   UnitPieces<4> pre4;
   // Double quant: the codes and absmax2 entries are staged instead of fp32
   // scales (code2 requested ahead of every copy) and converted before the loop.
-  const bool dq = !kResidual && p.absmax_q != nullptr;
+  constexpr bool dq = kDq;
   float dq_off = 0.f;
   DqStage dqs{};
   if (base) {
-    if (wave == 0 && dq) dq_issue_code2(p, dq_table, lane);  // ahead of wave 0's staging
+    if constexpr (dq) {
+      if (wave == 0) dq_issue_code2(p, dq_table, lane);  // ahead of wave 0's staging
+    }
     if (nb > 0) {
-      if (dq) {
+      if constexpr (dq) {
         dq_off = sload(p.dq_offset, 0);
         dqs = dq_stage(p, p.sc_bytes, kRows, lo, hi, kb0, nb);
         dq_issue(p, mysc, dqs, kRows, lo, hi, kb0, lane);
@@ -809,7 +814,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
     }
   }
 
-  if (dq) {
+  if constexpr (dq) {
     // The staging (and wave 0's code2 copies before it) was requested first:
     // it has landed once no more than the weight groups and x blocks
     // requested after it are outstanding (loads complete in issue order; a
@@ -995,10 +1000,10 @@ int64_t static_lds_of(K fn, int64_t& cache) {
 
 // Launches the variant whose static LDS and the waves' scale areas fit one
 // workgroup; returns false when it does not fit.
-template <bool kExact, int kDWG, bool kLora, bool kResidual = false>
+template <bool kExact, int kDWG, bool kLora, bool kResidual = false, bool kDq = false>
 bool try_launch(dim3 grid, hipStream_t s, const GemvParams& p, int64_t dyn) {
   static int64_t static_lds = -1;
-  auto fn = nf4_decode_wide_kernel<kExact, kDWG, kLora, kResidual>;
+  auto fn = nf4_decode_wide_kernel<kExact, kDWG, kLora, kResidual, kDq>;
   const int64_t st = static_lds_of(fn, static_lds);
   if (st < 0 || st + dyn > kLdsBytes) return false;
   hipLaunchKernelGGL(fn, grid, dim3(64 * (kBase + (kLora ? 1 : 0))), size_t(dyn), s, p);
@@ -1007,6 +1012,9 @@ bool try_launch(dim3 grid, hipStream_t s, const GemvParams& p, int64_t dyn) {
 
 template <bool kExact, bool kLora>
 bool launch_variant(dim3 grid, hipStream_t s, const GemvParams& p, int64_t dyn) {
+  if (p.absmax_q)
+    return try_launch<kExact, 2, kLora, false, true>(grid, s, p, dyn) ||
+           try_launch<kExact, 1, kLora, false, true>(grid, s, p, dyn);
   return try_launch<kExact, 2, kLora>(grid, s, p, dyn) || try_launch<kExact, 1, kLora>(grid, s, p, dyn);
 }
 
