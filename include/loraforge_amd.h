@@ -181,7 +181,7 @@ typedef struct lf_lora {
 } lf_lora;
 
 /* Bytes of device workspace lf_nf4_lora_linear needs for this problem. The
- * first 128 KiB are the decode kernel's control header (a launch word, a
+ * first 256 KiB are the decode kernel's control header (a launch word, a
  * status word and the shrink partials, each tagged with the call that wrote
  * it); it must be zero before the first call and is never reset between
  * calls. A prefill call uses the rest for its z rows and, for a double-quant

@@ -17,7 +17,7 @@ constexpr int kNf4Block = 64;
 // (entries are valid only for the call whose tag they carry, so nothing is
 // reset between calls). No other kernel writes it, so decode and prefill
 // calls can share one workspace.
-constexpr int64_t kWorkspaceHeader = 131072;
+constexpr int64_t kWorkspaceHeader = 262144;
 // The prefill's z flags follow the header at a fixed place: 4096 flags, one
 // per 256-token tile.
 constexpr int64_t kFlagRegion = 16384;

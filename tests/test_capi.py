@@ -60,8 +60,8 @@ def test_workspace_size_is_host_arithmetic():
     small = lib.lf_nf4_lora_workspace_size(1, 4096, 4096, 1, 16)
     big = lib.lf_nf4_lora_workspace_size(64, 4096, 4096, 1, 16)
     prefill = lib.lf_nf4_lora_workspace_size(2048, 11008, 4096, 1, 32)
-    # Decode: the 128 KiB control header (tagged shrink partials inside), the prefill's
+    # Decode: the 256 KiB control header (tagged shrink partials inside), the prefill's
     # 16 KiB flag region, then room for fp32 scales rebuilt from a nested state.
-    assert small == big == 131072 + 16384 + 4096 * (4096 // 64) * 4
-    assert prefill >= 131072 + 2048 * 64 * 2  # prefill z rows sit after that header
+    assert small == big == 262144 + 16384 + 4096 * (4096 // 64) * 4
+    assert prefill >= 262144 + 2048 * 64 * 2  # prefill z rows sit after that header
     assert lib.lf_nf4_lora_workspace_size(-1, 64, 64, 1, 1) == -1

@@ -27,7 +27,7 @@ from tests.test_fused_gpu import bits, close, to_device
 
 pytestmark = pytest.mark.gpu
 
-HEADER_BYTES = 131072  # the decode workspace's control header (no room for rebuilt scales)
+HEADER_BYTES = 262144  # the decode workspace's control header (no room for rebuilt scales)
 _WEIGHTS = {}
 
 
