@@ -286,6 +286,51 @@ def test_prefill_c5_shape_sampled(device):
     close(bits(y)[np.ix_(tokens, cols)], expect)
 
 
+def _torch_chain(x, w, lora, n):
+    """The fused linear's rounding chain in PyTorch fp32 on the GPU (no bias):
+    bf16(x W^T), z = bf16(x A_g^T), bf16(bf16(y) + bf16(scale_g z B_g^T)) per routed token."""
+    y = (x.float() @ w.float().t()).bfloat16().float()
+    slots = lora.token_slots.cpu().numpy()
+    ranks = lora.ranks.cpu().numpy()
+    a_off = lora.a_offsets.cpu().numpy()
+    b_off = lora.b_offsets.cpu().numpy()
+    strides = lora.b_strides.cpu().numpy()
+    scales = lora.scales.cpu().numpy()
+    k = x.shape[1]
+    for g in np.unique(slots[slots >= 0]):
+        r = int(ranks[g])
+        if r == 0:
+            continue
+        rows = torch.from_numpy(np.nonzero(slots == g)[0]).to(x.device)
+        a = lora.a_store[int(a_off[g]) : int(a_off[g]) + r * k].view(r, k).float()
+        b = lora.b_store[int(b_off[g]) : int(b_off[g]) + n * int(strides[g])].view(n, int(strides[g]))[:, :r].float()
+        z = (x[rows].float() @ a.t()).bfloat16().float()
+        delta = ((z @ b.t()) * float(scales[g])).bfloat16().float()
+        y[rows] = (y[rows] + delta).bfloat16().float()
+    return y.bfloat16()
+
+
+def test_prefill_c5_full_output_against_torch_fp32(device):
+    """Every element of the c5 output (2048 x 11008: both dispatch rounds of the 464 tiles, every
+    tile edge, the 8 segment boundaries) against the same rounding chain in PyTorch fp32 on the
+    GPU over the bit-exact dequantised weight (lf_nf4_dequant_dq, pinned by the oracle), at the
+    oracle tests' gate."""
+    from loraforge_amd.ops import dequantize_nf4_nested
+
+    m, n, k = 2048, 11008, 4096
+    rng = np.random.default_rng(736)
+    cuts = np.sort(rng.choice(np.arange(1, m), 7, replace=False))
+    lengths = np.diff(np.concatenate([[0], cuts, [m]]))
+    slots = np.repeat(np.arange(8, dtype=np.int32), lengths)
+    case = _cases.fused_case(m, n, k, ranks=(32,) * 8, double_quant=True, seed=736, token_slots=slots)
+    x, q, st, lora, _ = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, lora=lora)
+    w = dequantize_nf4_nested(q, st)
+    want = _torch_chain(x, w, lora, n)
+    torch.cuda.synchronize()
+    close(bits(y), bits(want))
+
+
 def test_decode_after_prefill_on_one_workspace(device):
     """Prefill and decode calls share one workspace: one call epoch, z rows clear of the header."""
     ws = torch.zeros(1 << 22, dtype=torch.uint8, device=device)
