@@ -174,8 +174,8 @@ typedef struct lf_lora {
   int32_t max_rank;           /* 1..64 */
   int32_t num_slots;          /* G, the entries of the per-slot arrays, or 0
                                  when not given. When given, token slots >= G
-                                 run base only, and with G <= 256 the decode
-                                 kernel for 33..64 tokens requests the per-slot
+                                 run base only, and with G <= 256 the wide
+                                 decode kernel (9..64 tokens) requests the per-slot
                                  arrays whole at its start, before it has read
                                  the tokens' slots. */
 } lf_lora;

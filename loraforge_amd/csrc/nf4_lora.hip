@@ -65,13 +65,13 @@ bool decode_chunks_cheaper(int64_t m, int64_t n, int64_t k, bool lora) {
   const double prefill_us = double(rounds) * 85.0 * double(k) / 4096.0 + (lora ? 20.0 : 0.0);
   return double(chunks) * chunk_us < prefill_us;
 }
-// One decode launch of up to 64 tokens: the wide kernel above 32 tokens when
-// it takes the shape, else the narrow one (the kernel a direct call of these
+// One decode launch of up to 64 tokens: the wide kernel for the batches and
+// shapes it takes (above 8 tokens, above 16 at K > 8192), else the narrow one (the kernel a direct call of these
 // rows would use, so each chunk of the chunked plan equals that call).
 int launch_decode(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                   const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
                   bool exact, bool swiglu, bool withhold, void* stream) {
-  if (m > 32 && decode_wide_fits(m, w->n, w->k, lora))
+  if (decode_wide_fits(m, w->n, w->k, lora))
     return launch_decode_wide(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
                               withhold, stream);
   return launch_nf4_gemv(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact, swiglu,
@@ -119,10 +119,10 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
     LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
   }
   const bool exact = (flags & LF_EXACT_WEIGHTS) != 0;
-  // Above 32 tokens: the wide decode kernel (one launch, base linear with or
+  // Above 8 tokens (16 at K > 8192): the wide decode kernel (one launch, base linear with or
   // without LoRA and the SwiGLU output), unless the prefill GEMM is forced or
   // cheaper, or the shape is outside the kernel's range.
-  if (m > 32 && lf::decode_wide_fits(m, n, k, lora) && !(flags & LF_PLAN_PREFILL) &&
+  if (lf::decode_wide_fits(m, n, k, lora) && !(flags & LF_PLAN_PREFILL) &&
       (m <= lf::kDecodeMaxTokens || (flags & LF_PLAN_DECODE_CHUNKS) || lf::wide_cheaper(m, n, k)))
     return lf::launch_decode_wide(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact,
                                   swiglu, withhold, stream);
@@ -143,8 +143,7 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
   if (!w->scales) {
     const int64_t last = m - (m - 1) / lf::kDecodeMaxTokens * lf::kDecodeMaxTokens;
     auto reads = [&](int64_t mc) {
-      return (mc > 32 && lf::decode_wide_fits(mc, n, k, lora)) ? lf::wide_takes_dq(w)
-                                                               : lf::gemv_takes_dq(mc, w, lora, exact);
+      return lf::decode_wide_fits(mc, n, k, lora) ? lf::wide_takes_dq(w) : lf::gemv_takes_dq(mc, w, lora, exact);
     };
     if (!reads(lf::kDecodeMaxTokens) || !reads(last)) {
       const int rc = lf::rebuild_decode_scales(w, workspace, workspace_bytes, stream, &wc.scales);

@@ -47,7 +47,7 @@ def test_decode_base_odd_shapes(m, n, k, device):
     close(bits(y), _base_expected(case))
 
 
-@pytest.mark.parametrize("m,with_lora", [(2, False), (2, True), (8, True), (20, True), (64, True)])
+@pytest.mark.parametrize("m,with_lora", [(2, False), (2, True), (8, True), (12, False), (20, True), (24, False), (64, True)])
 def test_decode_very_long_k(m, with_lora, device):
     """K = 131072: a wave's block scales no longer fit in LDS beside its ring, so
     the launch takes the variant that stages the scales with the weights (every

@@ -5,7 +5,7 @@ into LDS and converts them with the closed form of ``lf_nf4_dequant_dq``
 (reference ``ops/nf4.py:109-148``, the nested branch of ``prepare_scales``), so
 a call given the nested state (``scales="nested"``) must give exactly the bits
 of the same call given the prepared fp32 scales (whose path the oracle tests pin), in every
-narrow tile (1..32 tokens), the wide kernel (33..64), the chunked plan, with
+narrow tile (1..8 tokens, 9..16 at K = 12288), the wide kernel (the rest up to 64), the chunked plan, with
 and without LoRA, with the default and the exact-weights arithmetic. Through
 the C-ABI with a workspace of only the control header, the call can only
 succeed if the kernel read the state itself (a rebuild of fp32 scales needs
@@ -89,6 +89,21 @@ def test_nested_state_read_in_kernel(m, k, device):
             via_py = nf4_lora_linear(x, q, st, scales="nested", lora=lo, exact=exact)
             torch.cuda.synchronize()
             assert torch.equal(via_py, want)
+
+
+@pytest.mark.parametrize("m", [12, 24, 32])
+def test_nested_state_narrow_tiles_where_wide_declines(m, device):
+    """N = 448 with LoRA is no multiple of 256, so 9..32 tokens stay on the narrow kernel's
+    16- and 32-token tiles: the nested state read there in-kernel."""
+    n, k = 448, 4096
+    q, st = _weight(n, k, device, seed=13)
+    x, lora = _lora(m, n, k, device, seed=110 + m)
+    scales = prepare_scales(st)
+    for exact in (False, True):
+        got = _capi(x, q, st, lora, n, HEADER_BYTES, exact=exact)
+        want = nf4_lora_linear(x, q, st, scales=scales, lora=lora, exact=exact)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), exact
 
 
 @pytest.mark.parametrize("m", [1, 8, 48])

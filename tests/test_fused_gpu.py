@@ -109,6 +109,27 @@ def test_decode_batches(m, dq, device):
     workspace_clean(device)
 
 
+@pytest.mark.parametrize("m", [9, 12, 16, 17, 24, 32])
+def test_decode_narrow_tiles_where_wide_declines(m, device):
+    """9..32 tokens run the wide kernel where it takes the shape. With LoRA it needs N a
+    multiple of 256, so N = 448 keeps these batches on the narrow kernel's 16- and 32-token
+    tiles; without LoRA at K = 12288 the narrow kernel keeps 9..16 tokens (the wide one
+    takes 17..32)."""
+    ranks = (0, 4, 16, 33)
+    case = _cases.fused_case(m, 448, 1024, ranks=ranks, slices=2, bounds=[0, 192, 448], bias=True,
+                             double_quant=bool(m % 2), seed=300 + m)
+    x, q, st, lora, bias = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+    workspace_clean(device)
+    case = _cases.fused_case(m, 192, 12288, ranks=(1,), seed=400 + m, token_slots=[-1] * m)
+    x, q, st, _, _ = to_device(case, device)
+    y = nf4_lora_linear(x, q, st)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+
+
 def test_decode_mixed_ranks_slices_bias(device):
     ranks = (0, 1, 3, 8, 16, 17, 33, 64)
     bounds = [0, 320, 448, 512]
