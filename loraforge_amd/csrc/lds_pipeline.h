@@ -65,6 +65,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
 }
 
+// Adds one to a workgroup counter in LDS (a wave counting in). Through the
+// compiler, an LDS atomic after direct global -> LDS copies gets a vmcnt(0)
+// in front of it (the atomic is assumed to alias the copies' destinations),
+// which drains every copy in flight; the caller waits lgkmcnt(0) for its own
+// LDS writes first, and the counter is a location no copy writes.
+__device__ __forceinline__ void lds_count_in(int* counter) {
+  asm volatile("ds_add_u32 %0, %1" ::"v"(lds_addr(counter)), "v"(1) : "memory");
+}
+
 // Ties a value to the wait made before it: uses cannot be scheduled above.
 template <class T>
 __device__ __forceinline__ void tie(T& v) {

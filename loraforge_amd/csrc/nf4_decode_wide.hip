@@ -385,7 +385,7 @@ __device__ void unit_contract(const GemvParams& p, const Unit& un, float* red, i
     j0 += ps.rp;
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the partial rows are in LDS
-  if (lane == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (lane == 0) lds_count_in(done);
 }
 
 // A unit whose rows fit one pass and whose slice fits one group of c chunks
@@ -405,7 +405,7 @@ __device__ __forceinline__ void unit_contract_single(const UnitPieces<4>& pre, c
   if (lane < ps.rp) red[wave * 192 + lane] = 0.f;
   if ((lane & 7) == 0 && rsel < ps.pw) red[wave * 192 + (wave / ps.c) * ps.pw + rsel] = s;
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the partial rows are in LDS
-  if (lane == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (lane == 0) lds_count_in(done);
 }
 
 // Tile metadata of the wide kernel (the fields its base waves and the
@@ -771,7 +771,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
         for (int c = 0; c < kCP / 4; ++c) dst[c] = make_uint4(v, v, v, v);
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's entries are in LDS
-      if (lane == 0) __hip_atomic_fetch_add(&table_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (lane == 0) lds_count_in(&table_done);
     }
   } else {
     if (threadIdx.x == 0) {
