@@ -71,7 +71,15 @@ constexpr int kXSlot = kTokens * 128;  // one x block: 32 tokens x 64 bf16
 constexpr int kWGroup = kRows * 128;   // one weight group: 32 rows x 4 blocks x 32 packed bytes
 constexpr int kFirstSteps = 8;         // first-unit MFMA steps per base wave (8 x 8 covers a 2048-k slice)
 constexpr int kSlotsPerWave = kTokens / kBase;  // expand: the tile's distinct slots, one batch per wave
-constexpr int kContractAfter = 1;  // the loop block after which a producing wave contracts the first unit
+// The loop block after which a producing wave contracts the first unit. The
+// unit's pieces are requested behind the wave's first copies and, with the
+// whole chip's first burst of copies ahead of them, land about 2 us after its
+// first block: contracted after block 1 they held a producing wave's loop
+// there. Measured on MI355X (north star B = 64, us per call, two rounds of
+// alternating builds): after block 1 / 3 / 5 / 6 / 7 15.8 / 15.6 / 15.0 /
+// 15.4 / 15.6 (exact weights 16.6 / 16.3 / 16.0 / 16.5 / 16.9; c3 gate/up at
+// B = 64, three rounds of workgroups, about 1 us slower after block 5).
+constexpr int kContractAfter = 5;
 
 // Tile shape for the shared LoRA helpers (z staged for 32 tokens).
 struct WideTile {
@@ -800,8 +808,8 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
   }
   // A producing wave contracts its part of a single-pass first unit inside
   // the loop, after block kContractAfter: the pieces were requested before
-  // the refills of the blocks before it and have landed, and the loop is not
-  // held back until they do (a wave with fewer blocks contracts after the
+  // the refills of the blocks before it and have usually landed, and the loop
+  // is not held back until they do (a wave with fewer blocks contracts after the
   // loop). Longer units are contracted here, before the loop, so their
   // partials are not late for the other workgroups.
   bool contract = false;

@@ -144,7 +144,7 @@ def test_c3_chain_graph_replay(mlp_cases, device):
         assert torch.equal(y, eager)
 
 
-@pytest.mark.parametrize("m", [1, 2, 7, 16, 33, 64, 100])
+@pytest.mark.parametrize("m", [1, 2, 7, 16, 20, 33, 64, 100])
 @pytest.mark.parametrize("with_lora", [True, False])
 def test_fused_swiglu_output_equals_the_separate_chain(m, with_lora, device):
     """swiglu=True (decode: the activation in the kernel's epilogue, 16- and 32-row groups;
@@ -289,10 +289,10 @@ def test_fused_swiglu_graph_replay(device):
         assert torch.equal(out, eager)
 
 
-@pytest.mark.parametrize("m", [33, 48, 64])
+@pytest.mark.parametrize("m", [9, 24, 32, 33, 48, 64])
 def test_swiglu_flag_through_the_c_abi_at_32_row_groups(m, device):
-    """LF_SWIGLU_OUTPUT at 33..64 tokens (32-row groups: gate tile and up tile meet in LDS),
-    called through the C-ABI."""
+    """LF_SWIGLU_OUTPUT at 9..64 tokens (the wide kernel's 32-row groups: gate tile and up
+    tile meet in LDS; one token tile up to 32 tokens, two above), called through the C-ABI."""
     from loraforge_amd import _lib
     from loraforge_amd.ops.fused import _lora_struct, _weight_struct
 
