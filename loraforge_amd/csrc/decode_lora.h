@@ -74,6 +74,7 @@ struct GemvParams {
   int kz_len;     // k per slice (multiple of 64)
   int producers;  // workgroups b < producers make units b, b + producers, ...
   int resident;   // workgroups of the first dispatch round (b < resident run beside the producers)
+  int contract_after;  // (wide kernel) the loop block after which producing waves contract their first unit
   int* status;    // set to 1 when a bounded wait for partials gave up (they were then recomputed)
   int spin_limit; // polls of a bounded wait for partials
   int withhold;   // test hook: producers publish nothing, so every wait gives up and recomputes

@@ -71,15 +71,18 @@ constexpr int kXSlot = kTokens * 128;  // one x block: 32 tokens x 64 bf16
 constexpr int kWGroup = kRows * 128;   // one weight group: 32 rows x 4 blocks x 32 packed bytes
 constexpr int kFirstSteps = 8;         // first-unit MFMA steps per base wave (8 x 8 covers a 2048-k slice)
 constexpr int kSlotsPerWave = kTokens / kBase;  // expand: the tile's distinct slots, one batch per wave
-// The loop block after which a producing wave contracts the first unit. The
-// unit's pieces are requested behind the wave's first copies and, with the
-// whole chip's first burst of copies ahead of them, land about 2 us after its
-// first block: contracted after block 1 they held a producing wave's loop
-// there. Measured on MI355X (north star B = 64, us per call, two rounds of
+// The loop block after which a producing wave contracts the first unit
+// (GemvParams::contract_after). The unit's pieces are requested behind the
+// wave's first copies and, with the whole chip's first burst of copies ahead
+// of them, land about 2 us after its first block: in a grid of one dispatch
+// round, contracted after block 1 they held a producing wave's loop there.
+// Measured on MI355X (north star B = 64, us per call, two rounds of
 // alternating builds): after block 1 / 3 / 5 / 6 / 7 15.8 / 15.6 / 15.0 /
-// 15.4 / 15.6 (exact weights 16.6 / 16.3 / 16.0 / 16.5 / 16.9; c3 gate/up at
-// B = 64, three rounds of workgroups, about 1 us slower after block 5).
-constexpr int kContractAfter = 5;
+// 15.4 / 15.6 (exact weights 16.6 / 16.3 / 16.0 / 16.5 / 16.9). In grids of
+// several rounds (c3's gate/up at B = 64) block 1 stays ahead (about 1 us
+// per call), as the later rounds wait for nothing.
+constexpr int kContractAfterOneRound = 5;
+constexpr int kContractAfterRounds = 1;
 
 // Tile shape for the shared LoRA helpers (z staged for 32 tokens).
 struct WideTile {
@@ -807,7 +810,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
     while (*(const volatile __attribute__((address_space(3))) int*)(&table_done) < 4) __builtin_amdgcn_s_sleep(1);
   }
   // A producing wave contracts its part of a single-pass first unit inside
-  // the loop, after block kContractAfter: the pieces were requested before
+  // the loop, after block p.contract_after: the pieces were requested before
   // the refills of the blocks before it and have usually landed, and the loop
   // is not held back until they do (a wave with fewer blocks contracts after the
   // loop). Longer units are contracted here, before the loop, so their
@@ -908,7 +911,7 @@ __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_
         for (int e = 0; e < 16; ++e) acc[e] = __builtin_fmaf(sc, d[e], acc[e]);
       }
       if constexpr (kLora) {
-        if (bl == kContractAfter && contract) {
+        if (contract && bl == p.contract_after) {
           unit_contract_single(pre4, ps0, red, &prod_done, wave, lane);
           contract = false;
         }
@@ -1072,7 +1075,11 @@ GemvPlan wide_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
   pl.kz = int(kz);
   pl.kz_len = int((nblk + kz - 1) / kz) * 64;
   const int64_t groups = (zw + 3) / 4;  // 4-row groups per token
-  const int64_t split = std::max<int64_t>(1, std::min<int64_t>(groups, cap / (m * kz)));
+  // (Grids of several dispatch rounds: at most two units per token and
+  // slice, c3's gate/up at B = 64 about 2 us faster; one round: as many as
+  // the producers allow, B = 64 0.9 us faster than two.)
+  const int64_t split = std::max<int64_t>(
+      1, std::min<int64_t>({groups, cap / (m * kz), pl.grid > cus ? int64_t(2) : groups}));
   pl.urows = int((groups + split - 1) / split) * 4;
   pl.usplit = int((groups * 4 + pl.urows - 1) / pl.urows);
   pl.units = int(m) * pl.usplit * pl.kz;
@@ -1182,6 +1189,7 @@ int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_
     const GemvPlan pl = wide_plan(m, w->n, w->k, device_cus(), lora->num_slices * lora->max_rank);
     const int rc = fill_lora_params(p, pl, lora, m, workspace, workspace_bytes, withhold);
     if (rc != kOk) return rc;
+    p.contract_after = pl.grid > device_cus() ? kContractAfterRounds : kContractAfterOneRound;
   }
   const int64_t dyn = int64_t(kBase) * p.sc_bytes + 16 + (p.absmax_q ? 1024 : 0);
   const int64_t octets = (p.row_groups + 7) / 8;
