@@ -560,10 +560,9 @@ __device__ void gather_wide(const GemvParams& p, char* lds, const TokenMeta& m, 
 // before it counts the workgroup out of the call.
 __device__ __forceinline__ void lora_wave(const GemvParams& p, char* lora_lds, float* red, int* prod_done, int g_tile,
                                        int sbound, const SlotTable& stab, uint32_t epoch, int t0, int mt, int lane) {
-  // Issue priority over the two base waves that share this wave's SIMD: the
-  // chain below is short but serial, and at equal priority it gets about a
-  // third of the SIMD's issue slots while the base waves stream.
-  __builtin_amdgcn_s_setprio(3);
+  // (At the base waves' issue priority: raised to 3, as an earlier form of
+  // this chain was, c4 and c3's B = 64 MLP took about 0.9 us longer and the
+  // headline the same.)
   const TokenMeta tmeta =
       slot_table_usable(p) ? token_meta_from(p, stab, g_tile, mt, lane) : token_meta(p, g_tile, mt, lane);
   Unit un0{};
