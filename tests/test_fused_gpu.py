@@ -155,11 +155,14 @@ def test_decode_base_only_and_all_null_routes(device):
     close(bits(base), _cases.fused_expected(case))
 
 
-def test_decode_repeated_calls_and_graph_replay(device):
-    case = _cases.fused_case(8, 1024, 1024, ranks=(16,) * 4, seed=11)
+@pytest.mark.parametrize("m", [8, 20, 64])
+def test_decode_repeated_calls_and_graph_replay(m, device):
+    """Repeated calls on one workspace and graph replays give the eager bits: the narrow
+    kernel (8 tokens) and the wide one (one token tile at 20, two at 64)."""
+    case = _cases.fused_case(m, 1024, 1024, ranks=(16,) * 4, seed=11 + m)
     x, q, st, lora, _ = to_device(case, device)
     expect = _cases.fused_expected(case)
-    out = torch.empty(8, 1024, dtype=torch.bfloat16, device=device)
+    out = torch.empty(m, 1024, dtype=torch.bfloat16, device=device)
     for _ in range(5):
         nf4_lora_linear(x, q, st, lora=lora, out=out)
     torch.cuda.synchronize()
