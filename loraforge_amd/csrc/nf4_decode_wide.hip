@@ -10,10 +10,10 @@
 // A workgroup owns 32 output rows and 32 tokens over the whole K. Its eight
 // base waves split the NF4 blocks of K into contiguous ranges; each wave
 //   - requests the block scales of its whole range and the packed weight bytes
-//     of its first kDWG groups of four blocks (32 rows x 128 bytes: a full
-//     cache line of every row) at once, as direct global -> LDS copies that
-//     each read eight full lines, so the weight stream is in flight from the
-//     start; a group's slot is refilled as soon as its fourth block is read,
+//     of its first group of four blocks (32 rows x 128 bytes: a full cache
+//     line of every row) at once, as direct global -> LDS copies that each
+//     read eight full lines; the group's slot is refilled as soon as its
+//     fourth block is read (the launcher takes one slot, kDWG = 1),
 //   - streams the 32 token rows of x block by block through a private
 //     two-slot LDS ring (4 KiB per block: 32 tokens x 64 k),
 //   - contracts each block on v_mfma_f32_32x32x16_bf16 (tokens as A, the
@@ -578,7 +578,8 @@ __device__ __forceinline__ void lora_wave(const GemvParams& p, char* lora_lds, f
   depart_finish(p.ce, departed, __builtin_amdgcn_readfirstlane(epoch), lane);
 }
 
-// kDWG: weight group slots per wave (2, or 1 when a long K needs the LDS).
+// kDWG: weight group slots per wave (the launcher uses 1; the ring and its
+// waits are written for 1 or 2).
 // kLora: a ninth wave and the LoRA stages (row groups must fill whole XCD
 // octets, so every workgroup of the grid is a real one and counts in once).
 // kResidual (with kLora): no weight; y is the base and is updated in place
@@ -589,7 +590,7 @@ template <bool kExact, int kDWG, bool kLora, bool kResidual = false, bool kDq = 
 __global__ __launch_bounds__(64 * (kBase + (kLora ? 1 : 0)), 1) void nf4_decode_wide_kernel(GemvParams p) {
   static_assert(!kResidual || (kLora && !kExact), "the residual form is a LoRA-only variant");
   static_assert(!(kResidual && kDq), "the residual form reads no weight");
-  constexpr int kCP = kLora ? 8 : 16;  // pair-table copies (lane l reads copy l % kCP); 8 leave LDS for LoRA
+  constexpr int kCP = 16;  // pair-table copies (lane l reads copy l % kCP)
   __shared__ __attribute__((aligned(16))) char wring[kBase * kDWG * kWGroup];
   __shared__ __attribute__((aligned(16))) char xring[kBase * kDX * kXSlot];
   __shared__ float table[16];
@@ -1021,11 +1022,19 @@ bool try_launch(dim3 grid, hipStream_t s, const GemvParams& p, int64_t dyn) {
 }
 
 template <bool kExact, bool kLora>
+// One weight-group slot per wave at every K (the second group is requested
+// after the first one's fourth block), which also leaves the LDS for 16
+// pair-table copies with LoRA. Measured on MI355X against two slots (the
+// whole W of a wave at K = 4096 requested up front) and 8 copies with LoRA:
+// headline 15.5 -> 14.7 us, north star B = 16 / 32 / 64 14.2 / 14.6 / 15.1
+// -> 13.5 / 14.2 / 14.3-14.8 us, base only B = 64 10.1 -> 9.8 us, exact
+// weights B = 64 16.1 -> 15.7 us, c4 66.3 -> 64.4 us, c3 B = 64 98.5 -> 94.7
+// us; with two slots and 8 copies the loop's LDS reads conflicted more and
+// the up-front weight requests queued ahead of the x blocks. 32 copies were
+// slower again (headline 15.1 us).
 bool launch_variant(dim3 grid, hipStream_t s, const GemvParams& p, int64_t dyn) {
-  if (p.absmax_q)
-    return try_launch<kExact, 2, kLora, false, true>(grid, s, p, dyn) ||
-           try_launch<kExact, 1, kLora, false, true>(grid, s, p, dyn);
-  return try_launch<kExact, 2, kLora>(grid, s, p, dyn) || try_launch<kExact, 1, kLora>(grid, s, p, dyn);
+  if (p.absmax_q) return try_launch<kExact, 1, kLora, false, true>(grid, s, p, dyn);
+  return try_launch<kExact, 1, kLora>(grid, s, p, dyn);
 }
 
 // Floats per row of a wave's scale area: the wave's blocks rounded up to a
