@@ -70,14 +70,15 @@ LAYERS = 64
 ROUNDS = 3
 
 TRAFFIC_FILE = ROOT / "profiles" / "decode_hbm_traffic.json"
-# The kernel that runs a decode batch at K = 4096: 1..8 tokens the narrow decode
-# kernel, 9..64 the wide one (32 rows x 32 tokens per workgroup).
+# The kernel that runs a decode batch of the headline shape (N = K = 4096): 1..8
+# tokens the narrow decode kernel, 9..64 the wide one (32 rows x 32 tokens per
+# workgroup).
 NARROW_SOURCE = ROOT / "loraforge_amd" / "csrc" / "nf4_gemv.hip"
 WIDE_SOURCE = ROOT / "loraforge_amd" / "csrc" / "nf4_decode_wide.hip"
 
 
 def decode_kernel(batch: int) -> tuple[str, Path]:
-    # The library's routing at K = 4096: the wide kernel above 8 tokens.
+    # The library's routing at N = K = 4096: the wide kernel above 8 tokens.
     return ("nf4_decode_wide_kernel", WIDE_SOURCE) if batch > 8 else ("nf4_gemv_kernel", NARROW_SOURCE)
 
 

@@ -175,9 +175,10 @@ typedef struct lf_lora {
   int32_t num_slots;          /* G, the entries of the per-slot arrays, or 0
                                  when not given. When given, token slots >= G
                                  run base only, and with G <= 256 the wide
-                                 decode kernel (9..64 tokens) requests the per-slot
-                                 arrays whole at its start, before it has read
-                                 the tokens' slots. */
+                                 decode kernel (9..64 tokens; 3..64 at
+                                 N >= 8192) requests the per-slot arrays
+                                 whole at its start, before it has read the
+                                 tokens' slots. */
 } lf_lora;
 
 /* Bytes of device workspace lf_nf4_lora_linear needs for this problem. The

@@ -1,5 +1,5 @@
 // Wide-batch NF4 decode linear with per-token multi-LoRA (more than 8 tokens,
-// more than 16 at K > 8192; one launch for any batch whose 32-token tiles the chip can take in a few
+// more than 2 at N >= 8192, more than 16 at K > 8192; one launch for any batch whose 32-token tiles the chip can take in a few
 // rounds).
 //
 // Reference chain (integrations/_sglang_nf4_linear.py:116-129, then the row
@@ -1096,15 +1096,22 @@ GemvPlan wide_plan(int64_t m, int64_t n, int64_t k, int cus, int zw) {
 }
 
 // Batches the wide kernel serves faster than the narrow one (measured on
-// MI355X, us per call with 32 rank-16 adapters; narrow / wide):
-//   4096 x 4096 at 12 / 16 / 24 / 32 tokens: 15.0 / 15.0 / 16.2 / 16.6
-//     against 13.8 / 14.1 / 14.5 / 14.6 (9 tokens: 14.3 / 13.5);
-//   24576 x 4096: 58.8 / 62.7 / 69.8 / 72.9 against 37.7 / 38.6 / 39.7 / 40.7;
-//   4096 x 12288: 24.0 / 24.9 / 33.5 / 35.2 against 25.6 / 26.1 / 27.0 / 28.8
-//     (128 workgroups with one weight slot a wave: long K keeps the narrow
-//     kernel up to 16 tokens).
-// Up to 8 tokens the narrow kernel runs two workgroups per CU and wins.
-bool wide_takes_batch(int64_t m, int64_t k) { return m > 16 || (m > 8 && k <= 8192); }
+// MI355X with one weight slot and 16 table copies, us per call with 32
+// rank-16 adapters; narrow / wide):
+//   4096 x 4096 at 2 / 4 / 8 / 12 / 16 / 24 tokens: 10.1 / 11.2 / 11.6 /
+//     15.2 / 14.8 / 16.4 against 12.6 / 12.7 / 13.1 / 13.2 / 13.5 / 13.8;
+//   N = 8192 / 12288 / 16384 / 24576 (K = 4096) at 2 tokens: 12.8 / 20.1 /
+//     21.6 / 30.8 against 13.1 / 19.7 / 22.5 / 32.1; at 3: 13.4 / 21.9 /
+//     23.8 / 33.4 against 13.3 / 19.9 / 22.7 / 32.2; at 8: 14.5 / 24.1 /
+//     25.8 / 36.6 against 13.6 / 21.0 / 24.2 / 34.3 (the narrow kernel's
+//     two workgroups per CU win while one round of them covers N);
+//   4096 x 12288 at 4 / 8 / 12 / 16 / 24: 17.1 / 21.1 / 23.7 / 24.9 / 33.3
+//     against 23.1 / 23.8 / 24.5 / 24.9 / 26.2 (128 workgroups with one
+//     weight slot a wave: long K keeps the narrow kernel up to 16 tokens).
+bool wide_takes_batch(int64_t m, int64_t n, int64_t k) {
+  if (k > 8192) return m > 16;
+  return m > 8 || (m > 2 && n >= 8192);
+}
 
 // Whether the wide decode kernel takes this call: a batch it serves faster
 // (wide_takes_batch), a K whose rings and scale areas fit LDS (the smallest
@@ -1112,7 +1119,7 @@ bool wide_takes_batch(int64_t m, int64_t k) { return m > 16 || (m > 8 && k <= 81
 // of 256), shrink partials that fit the workspace header and at most 1024
 // units.
 bool decode_wide_fits(int64_t m, int64_t n, int64_t k, const lf_lora* lora) {
-  if (!wide_takes_batch(m, k) || n % kRows) return false;
+  if (!wide_takes_batch(m, n, k) || n % kRows) return false;
   const int64_t nblk = k / 64;
   const int64_t area = scale_area_bytes(nblk);
   // Static LDS of the smallest variant: one weight group and two x blocks per

@@ -66,8 +66,9 @@ bool decode_chunks_cheaper(int64_t m, int64_t n, int64_t k, bool lora) {
   return double(chunks) * chunk_us < prefill_us;
 }
 // One decode launch of up to 64 tokens: the wide kernel for the batches and
-// shapes it takes (above 8 tokens, above 16 at K > 8192), else the narrow one (the kernel a direct call of these
-// rows would use, so each chunk of the chunked plan equals that call).
+// shapes it takes (above 8 tokens, above 2 at N >= 8192, above 16 at
+// K > 8192), else the narrow one (the kernel a direct call of these rows
+// would use, so each chunk of the chunked plan equals that call).
 int launch_decode(const uint16_t* x, int64_t m, int64_t x_stride, const lf_nf4_weight* w, const uint16_t* bias,
                   const lf_lora* lora, uint16_t* y, int64_t y_stride, void* workspace, int64_t workspace_bytes,
                   bool exact, bool swiglu, bool withhold, void* stream) {
@@ -119,9 +120,10 @@ extern "C" int lf_nf4_lora_linear(const uint16_t* x, int64_t m, int64_t x_stride
     LF_REQUIRE(lf::aligned16(lora->a_store) && lf::aligned16(lora->b_store), "A/B stores must be 16-byte aligned");
   }
   const bool exact = (flags & LF_EXACT_WEIGHTS) != 0;
-  // Above 8 tokens (16 at K > 8192): the wide decode kernel (one launch, base linear with or
-  // without LoRA and the SwiGLU output), unless the prefill GEMM is forced or
-  // cheaper, or the shape is outside the kernel's range.
+  // Above 8 tokens (2 at N >= 8192, 16 at K > 8192): the wide decode kernel
+  // (one launch, base linear with or without LoRA and the SwiGLU output),
+  // unless the prefill GEMM is forced or cheaper, or the shape is outside the
+  // kernel's range.
   if (lf::decode_wide_fits(m, n, k, lora) && !(flags & LF_PLAN_PREFILL) &&
       (m <= lf::kDecodeMaxTokens || (flags & LF_PLAN_DECODE_CHUNKS) || lf::wide_cheaper(m, n, k)))
     return lf::launch_decode_wide(x, m, x_stride, w, bias, lora, y, y_stride, workspace, workspace_bytes, exact,
