@@ -109,6 +109,22 @@ def test_decode_batches(m, dq, device):
     workspace_clean(device)
 
 
+@pytest.mark.parametrize("m", [3, 5, 8])
+def test_decode_small_batches_on_wide_rows(m, device):
+    """3..8 tokens at N >= 8192 run the wide kernel (one token tile, 32-row groups):
+    with LoRA (slices, bias, base-only tokens) and without, against the oracle."""
+    case = _cases.fused_case(m, 8192, 1024, ranks=(0, 8, 16, 32), slices=2, bounds=[0, 4096, 8192], bias=True,
+                             seed=500 + m, null_frac=0.3)
+    x, q, st, lora, bias = to_device(case, device)
+    y = nf4_lora_linear(x, q, st, bias=bias, lora=lora)
+    torch.cuda.synchronize()
+    close(bits(y), _cases.fused_expected(case))
+    workspace_clean(device)
+    base = nf4_lora_linear(x, q, st, bias=bias)
+    torch.cuda.synchronize()
+    close(bits(base), _cases.fused_expected(dict(case, lora=dict(case["lora"], token_slots=np.full(m, -1, np.int32)))))
+
+
 @pytest.mark.parametrize("m", [9, 12, 16, 17, 24, 32])
 def test_decode_narrow_tiles_where_wide_declines(m, device):
     """9..32 tokens run the wide kernel where it takes the shape. With LoRA it needs N a
