@@ -81,7 +81,11 @@ constexpr int kSlotsPerWave = kTokens / kBase;  // expand: the tile's distinct s
 // 15.4 / 15.6 (exact weights 16.6 / 16.3 / 16.0 / 16.5 / 16.9). In grids of
 // several rounds (c3's gate/up at B = 64) block 1 stays ahead (about 1 us
 // per call), as the later rounds wait for nothing.
+// One weight slot per wave (us per call, north star): a full round (B = 64,
+// 256 workgroups) after block 3 / 4 / 5 / 6 14.5 / 14.3 / 14.1 / 14.4; a
+// partial round (B = 32, 128 workgroups) 13.8 / 13.9 / 14.2 / 14.4.
 constexpr int kContractAfterOneRound = 5;
+constexpr int kContractAfterPartialRound = 3;
 constexpr int kContractAfterRounds = 1;
 
 // Tile shape for the shared LoRA helpers (z staged for 32 tokens).
@@ -1204,7 +1208,10 @@ int launch_decode_wide(const uint16_t* x, int64_t m, int64_t x_stride, const lf_
     const GemvPlan pl = wide_plan(m, w->n, w->k, device_cus(), lora->num_slices * lora->max_rank);
     const int rc = fill_lora_params(p, pl, lora, m, workspace, workspace_bytes, withhold);
     if (rc != kOk) return rc;
-    p.contract_after = pl.grid > device_cus() ? kContractAfterRounds : kContractAfterOneRound;
+    const int64_t cus = device_cus();
+    p.contract_after = pl.grid > cus    ? kContractAfterRounds
+                       : pl.grid >= cus ? kContractAfterOneRound
+                                        : kContractAfterPartialRound;
   }
   const int64_t dyn = int64_t(kBase) * p.sc_bytes + 16 + (p.absmax_q ? 1024 : 0);
   const int64_t octets = (p.row_groups + 7) / 8;
